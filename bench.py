@@ -1,0 +1,187 @@
+"""Benchmark of the ZeRO-1 shard optimizer update on one MI355X.
+
+A step is one optimizer update of one GPU's shard with its inputs resident in HBM: sum of squares -> norm + clip
+factor -> Adam + BF16 copy (config c3 adds the fused owner sum of 8 BF16 contributions in front, replacing the
+sum of squares).  Default workload: c2, the 430,662,912-parameter YOCO-3B shard.
+
+Prints ONE JSON line: ms per step (the metric), the Adam kernel's roofline from HIP events recorded on the
+launch stream, and the PyTorch-CPU restatement's time on a bounded sample of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--config c2] [--cpu-sample-tensors T] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PEAK_HBM_GBPS = 8000.0
+WORKLOADS = {
+    'c1': 'C1 plumbing: 4 fp32 tensors, 9,438,208 params, step 1 (cache-resident; not graded)',
+    'c2': 'C2 YOCO-3B ZeRO-1 shard: 430,662,912 params in 38 fp32 tensors, step 1000',
+    'c3': 'C3 owner reduce: 8 bf16 contributions of the C2 shard summed in rank order, fused norm, Adam on bf16 g',
+    'c4': 'C4 unsharded YOCO-3B: 3,445,303,296 params in 304 fp32 tensors, step 1000',
+    'c5': 'C5 C2 with Student-t(2) gradients and 0.1% +-1e4 outliers (clip active)',
+}
+
+
+def algorithmic_bytes(cfg, n):
+    """(bytes per step, Adam bytes per launch, Adam bytes per param) from the per-parameter stream sizes."""
+    if cfg == 'c3':
+        return 46 * n, 28 * n, 28        # owner sum (16 in + 2 out) + Adam with bf16 g (g 2 + p,m,v 12 + 12 + p16 2)
+    return 34 * n, 30 * n, 30            # norm (4) + Adam with fp32 g (16 in, 12 out, 2 bf16 out)
+
+
+def load_traffic(kernel, workload):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), from a
+    committed summary under profiles/, or None."""
+    path = os.path.join(ROOT, 'profiles', f'{kernel}_{workload}_traffic.json')
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        d = json.load(f)
+    return d.get('hbm_bytes_per_launch')
+
+
+def cpu_baseline(shard, cfg, ntensors, contribs, hp, step, threads):
+    """Times the PyTorch-CPU restatement (oracle/torch_cpu.py) on the first `ntensors` tensors of the same shard
+    (copied from the GPU buffers), 1 warm-up + median of 3, scaled to the whole shard by parameter count."""
+    import torch
+    sys.path.insert(0, ROOT)
+    from oracle import torch_cpu
+    torch.set_num_threads(threads)
+    k = min(ntensors, len(shard.numels))
+    n_s = sum(shard.numels[:k])
+    end = shard.offsets[k - 1] + shard.numels[k - 1]
+    host = {b: getattr(shard, b)[:end].cpu() for b in ('p', 'm', 'v')}
+    g_host = shard.g[:end].float().cpu() if cfg != 'c3' else None
+    c_host = [c[:end].cpu() for c in contribs] if cfg == 'c3' else None
+
+    def views(buf):
+        return [buf[o:o + n] for o, n in zip(shard.offsets[:k], shard.numels[:k])]
+
+    times = []
+    for it in range(4):
+        p, m, v = host['p'].clone(), host['m'].clone(), host['v'].clone()
+        g = g_host.clone() if g_host is not None else torch.empty(end, dtype=torch.float32)
+        p16 = torch.empty(end, dtype=torch.bfloat16)
+        t0 = time.perf_counter()
+        torch_cpu.update(views(g), views(p), views(m), views(v), views(p16), lr=hp['lr'], betas=hp['betas'],
+                         eps=hp['eps'], weight_decay=hp['weight_decay'], step=step, max_norm=hp['max_norm'],
+                         contribs=c_host)
+        t1 = time.perf_counter()
+        if it:
+            times.append(t1 - t0)
+    times.sort()
+    ms_sample = times[len(times) // 2] * 1e3
+    return {'value': round(ms_sample * shard.numel / n_s, 3), 'unit': 'ms per full-shard step (scaled)',
+            'cores': threads, 'kind': 'port',
+            'sample': f'first {k} tensors of the same {cfg} shard ({n_s:,} of {shard.numel:,} params), '
+                      f'median of 3 after 1 warm-up = {ms_sample:.1f} ms, scaled by parameter count; '
+                      f'torch {torch.__version__} CPU, os.cpu_count()={os.cpu_count()}'}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument('--gpus', type=int, default=1)
+    ap.add_argument('--steps', type=int, default=20)
+    ap.add_argument('--warmup', type=int, default=3)
+    ap.add_argument('--config', default='c2', choices=sorted(WORKLOADS))
+    ap.add_argument('--cpu-sample-tensors', type=int, default=6)
+    ap.add_argument('--no-cpu-baseline', action='store_true')
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
+        print('bench.py: this build measures one GPU only (the shard update of one ZeRO-1 owner); '
+              '--gpus must be 1', file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, ROOT)
+    import __graft_entry__
+    __graft_entry__.package()
+    from faster_yoco_amd import configs, shard as shard_mod
+
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    cfg = args.config
+    hp = configs.HPARAMS
+    gdt = torch.bfloat16 if cfg == 'c3' else torch.float32
+    shard = shard_mod.FlatShard(configs.shapes(cfg), dev, grad_dtype=gdt)
+    contribs = configs.fill_shard(shard, cfg, seed=0)
+    step0 = configs.CONFIGS[cfg]['step']
+    opt = shard_mod.Zero1ShardOptimizer(shard, lr=hp['lr'], betas=hp['betas'], eps=hp['eps'],
+                                        weight_decay=hp['weight_decay'])
+    opt.step_count = step0 - 1
+    torch.cuda.synchronize()
+
+    # the CPU baseline copies the pre-update state, so it runs before the GPU steps mutate it
+    cpu = None
+    if not args.no_cpu_baseline:
+        threads = len(os.sched_getaffinity(0))
+        cpu = cpu_baseline(shard, cfg, args.cpu_sample_tensors, contribs, hp, step0, threads)
+        print(f'# cpu baseline done: {cpu["sample"]}', file=sys.stderr, flush=True)
+
+    def one_step(ev=None):
+        if ev is not None:
+            ev[0].record()
+        if contribs is not None:
+            opt.reduce_grads(contribs)
+        opt.clip_grad_norm(hp['max_norm'])
+        if ev is not None:
+            ev[1].record()
+        opt.step()
+        if ev is not None:
+            ev[2].record()
+
+    for _ in range(args.warmup):
+        one_step()
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        one_step(events[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+
+    ms_step = wall * 1e3 / args.steps
+    adam_ms = [e[1].elapsed_time(e[2]) for e in events]
+    pre_ms = [e[0].elapsed_time(e[1]) for e in events]
+    adam_avg = sum(adam_ms) / len(adam_ms)
+    n = shard.numel
+    step_bytes, adam_bytes, adam_bpp = algorithmic_bytes(cfg, n)
+    achieved = adam_bytes / (adam_avg * 1e-3) / 1e9
+    out = {
+        'metric': 'ms per optimizer step (431M-param shard); achieved HBM GB/s vs ~8 TB/s peak',
+        'value': round(ms_step, 4),
+        'unit': 'ms',
+        'n_gpus': 1,
+        'steps': args.steps,
+        'warmup': args.warmup,
+        'ms_per_step': round(ms_step, 4),
+        'higher_is_better': False,
+        'scaling': 'weak',
+        'vs_baseline': None,
+        'dtype': 'fp32',
+        'data': 'synthetic (seeded torch generator on the device; no checkpoint)',
+        'config': {'workload': WORKLOADS[cfg], 'config': cfg, 'params': n, 'tensors': len(shard.numels),
+                   'grad_dtype': str(gdt).replace('torch.', ''), 'lr': hp['lr'], 'betas': list(hp['betas']),
+                   'eps': hp['eps'], 'weight_decay': hp['weight_decay'], 'max_norm': hp['max_norm'],
+                   'algorithmic_bytes_per_step': step_bytes},
+        'achieved_GBps': round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
+        'frac_of_peak': round(step_bytes / (ms_step * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+        'kernel_ms': {'adam_cast': round(adam_avg, 4),
+                      ('owner_sum+norm_clip' if cfg == 'c3' else 'sumsq+norm_clip'): round(sum(pre_ms) / len(pre_ms), 4)},
+        'roofline': {'bound': 'hbm', 'kernel': 'adam_cast_kernel', 'achieved': round(achieved, 1),
+                     'peak': PEAK_HBM_GBPS, 'unit': 'GB/s', 'frac': round(achieved / PEAK_HBM_GBPS, 4),
+                     'traffic': load_traffic('adam_cast', cfg),
+                     'bytes_per_param': adam_bpp, 'params_per_launch': n},
+        'cpu_baseline': cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == '__main__':
+    main()

@@ -1,0 +1,16 @@
+"""faster-yoco_amd: MI355X-native owner-side ZeRO-1 optimizer update for one GPU's shard.
+
+The directory name is not a Python identifier; the package is imported as ``faster_yoco_amd`` through
+``__graft_entry__.package()`` (or any loader that registers it under that name).
+
+Modules
+    ops              torch-tensor wrappers over the C ABI of libyoco_z1.so (include/yoco_z1.h)
+    shard            flat HBM shard + FP16Optimizer-style optimizer (multiply_grads / clip_grad_norm / step)
+    fused_adam_cast  drop-in for yoco/tasks/fused_adam_cast.py (FusedAdamCast, scale_up)
+    zero1_fast       drop-in for yoco/tasks/zero1_fast.py (clip_grad_norm / step / zero_grad patches, layout)
+    ce_reduce        drop-in for the owner-sum kernel of yoco/models/decoder/ce_reduce.py (_sum_slots, _sum)
+    configs          the benchmark/parity workloads (tensor lists and synthetic inputs)
+"""
+from . import _lib, ops  # noqa: F401
+
+__all__ = ['ops', 'shard', 'fused_adam_cast', 'zero1_fast', 'ce_reduce', 'configs', 'layout']

@@ -1,0 +1,166 @@
+"""The five workloads of the benchmark and parity suite: tensor lists, hyperparameters and synthetic inputs.
+
+C1  plumbing: 4 tensors, 9,438,208 params, step 1 from m = v = 0
+C2  one GPU's YOCO-3B ZeRO-1 shard: 430,662,912 params in 38 tensors, step 1000
+C3  C2 fed by 8 BF16 owner-side contributions summed in rank order (fused owner sum + norm)
+C4  the unsharded YOCO-3B update: C2's list x 8 = 304 tensors, 3,445,303,296 params
+C5  C2 with heavy-tailed (Student-t nu=2) gradients and 0.1% +-1e4 outliers (clip coefficient << 1)
+
+Inputs are synthetic.  GPU inputs come from torch's seeded generator on the device (``fill_shard``); small parity
+inputs come from NumPy's seeded PCG64 on the host (``host_inputs``) so the oracle sees the same arrays.
+"""
+import math
+
+import numpy as np
+import torch
+
+HPARAMS = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_norm=1.0)
+
+C1_SHAPES = [(1024, 1024), (4096, 1024), (1024, 4096), (1024,)]
+C1_MINI_SHAPES = [(64, 64), (256, 64), (64, 256), (64,)]
+
+DIM, HIDDEN = 3072, 8192
+
+
+def c2_shapes():
+    """38 tensors, 430,662,912 = 3,445,303,296 / 8 params: ([3072,3072], [8192,3072], [3072]) x 12, then
+    [3072,3072], then a 1-D tail of 5,952,768 elements."""
+    s = [(DIM, DIM), (HIDDEN, DIM), (DIM,)] * 12 + [(DIM, DIM), (5_952_768,)]
+    assert sum(math.prod(x) for x in s) == 430_662_912
+    return s
+
+
+def c4_shapes():
+    """304 tensors, 3,445,303,296 params."""
+    return c2_shapes() * 8
+
+
+CONFIGS = {
+    'c1': dict(shapes=C1_SHAPES, step=1, grad='normal', g_std=1e-3, m_std=0.0, v_std=0.0),
+    'c2': dict(shapes=None, step=1000, grad='normal', g_std=1e-4, m_std=1e-4, v_std=1e-8),
+    'c3': dict(shapes=None, step=1000, grad='owner8', g_std=1e-4, m_std=1e-4, v_std=1e-8),
+    'c4': dict(shapes=None, step=1000, grad='normal', g_std=1e-4, m_std=1e-4, v_std=1e-8),
+    'c5': dict(shapes=None, step=1000, grad='student_t', g_std=1e-3, m_std=1e-4, v_std=1e-8),
+}
+
+
+def shapes(name):
+    if name == 'c1':
+        return list(C1_SHAPES)
+    if name in ('c2', 'c3', 'c5'):
+        return c2_shapes()
+    if name == 'c4':
+        return c4_shapes()
+    raise KeyError(name)
+
+
+def numel(name):
+    return sum(math.prod(s) for s in shapes(name))
+
+
+# ---------------------------------------------------------------------------------------------------- device
+def _gen(device, seed):
+    g = torch.Generator(device=device)
+    g.manual_seed(int(seed))
+    return g
+
+
+def _normal_(t, std, gen, chunk=1 << 26):
+    for i in range(0, t.numel(), chunk):
+        t[i:i + chunk].normal_(0.0, std, generator=gen)
+    return t
+
+
+def student_t2_(t, scale, gen, chunk=1 << 26):
+    """t = scale * (2u-1)/sqrt(2u(1-u)), u uniform in (0,1): Student-t with nu = 2 by its closed-form inverse CDF."""
+    for i in range(0, t.numel(), chunk):
+        u = torch.rand(min(chunk, t.numel() - i), dtype=torch.float64, device=t.device, generator=gen)
+        u = u.clamp_(2.0 ** -30, 1.0 - 2.0 ** -30)
+        t[i:i + chunk] = ((2.0 * u - 1.0) / torch.sqrt(2.0 * u * (1.0 - u)) * scale).to(t.dtype)
+    return t
+
+
+def outliers_(t, frac, value, gen):
+    """Sets round(frac * n) distinct entries to +-value (sign random)."""
+    n = t.numel()
+    k = int(round(frac * n))
+    if k == 0:
+        return t
+    idx = torch.randperm(n, device=t.device, generator=gen)[:k]
+    sign = torch.randint(0, 2, (k,), device=t.device, generator=gen).to(t.dtype) * 2 - 1
+    t[idx] = sign * value
+    return t
+
+
+def fill_shard(shard, name, seed=0):
+    """Synthetic state for config `name` written into a FlatShard on its device: p ~ N(0, 0.02), m, v and g per
+    the config.  Returns the owner-side contributions (list of bf16 flat tensors) for 'c3', else None."""
+    cfg = CONFIGS[name]
+    gen = _gen(shard.device, seed)
+    _normal_(shard.p, 0.02, gen)
+    if cfg['m_std'] > 0:
+        _normal_(shard.m, cfg['m_std'], gen)
+    else:
+        shard.m.zero_()
+    if cfg['v_std'] > 0:
+        _normal_(shard.v, cfg['v_std'], gen).abs_()
+    else:
+        shard.v.zero_()
+    if shard.p16 is not None:
+        shard.p16.copy_(shard.p)
+    if cfg['grad'] == 'owner8':
+        contribs = []
+        for r in range(8):
+            c = torch.empty(shard.total, dtype=torch.float32, device=shard.device)
+            _normal_(c, cfg['g_std'], _gen(shard.device, seed + 1 + r))
+            contribs.append(c.to(torch.bfloat16))
+            del c
+        shard.g.zero_()
+        return contribs
+    if cfg['grad'] == 'student_t':
+        student_t2_(shard.g, cfg['g_std'], gen)
+        outliers_(shard.g, 1e-3, 1e4, gen)
+    else:
+        _normal_(shard.g, cfg['g_std'], gen)
+    return None
+
+
+# ------------------------------------------------------------------------------------------------------ host
+def host_inputs(n, name='c1', seed=0):
+    """NumPy inputs of n elements for config `name`: dict with g (float32), p, m, v and, for 'c3', 'contribs'
+    (8 uint16 bf16 arrays).  Used by the parity tests, where the oracle must see exactly the GPU's inputs."""
+    cfg = CONFIGS[name]
+    rng = np.random.default_rng(seed)
+    out = {'p': (rng.standard_normal(n) * 0.02).astype(np.float32)}
+    out['m'] = (rng.standard_normal(n) * cfg['m_std']).astype(np.float32) if cfg['m_std'] > 0 else \
+        np.zeros(n, np.float32)
+    out['v'] = np.abs(rng.standard_normal(n) * cfg['v_std']).astype(np.float32) if cfg['v_std'] > 0 else \
+        np.zeros(n, np.float32)
+    if cfg['grad'] == 'student_t':
+        u = (rng.integers(0, 1 << 24, n).astype(np.float64) + 0.5) / float(1 << 24)
+        g = (2.0 * u - 1.0) / np.sqrt(2.0 * u * (1.0 - u)) * cfg['g_std']
+        k = int(round(1e-3 * n))
+        if k:
+            idx = rng.choice(n, size=k, replace=False)
+            g[idx] = np.where(rng.integers(0, 2, k) == 1, 1e4, -1e4)
+        out['g'] = g.astype(np.float32)
+    else:
+        out['g'] = (rng.standard_normal(n) * cfg['g_std']).astype(np.float32)
+    if cfg['grad'] == 'owner8':
+        contribs = []
+        for r in range(8):
+            c = (np.random.default_rng(seed + 1 + r).standard_normal(n) * cfg['g_std']).astype(np.float32)
+            u = c.view(np.uint32).astype(np.uint64)
+            contribs.append(((u + 0x7fff + ((u >> 16) & 1)) >> 16).astype(np.uint16))
+        out['contribs'] = contribs
+    return out
+
+
+def to_device_bf16(h, device):
+    """uint16 bf16 bits (NumPy) -> bf16 device tensor."""
+    return torch.from_numpy(np.ascontiguousarray(h).view(np.int16)).to(device).view(torch.bfloat16)
+
+
+def bf16_bits(t):
+    """bf16 tensor -> uint16 NumPy bits (host copy)."""
+    return t.detach().view(torch.int16).cpu().numpy().view(np.uint16)

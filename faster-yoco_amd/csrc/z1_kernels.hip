@@ -1,0 +1,718 @@
+// yoco_z1: gfx950 kernels + C ABI for the owner-side ZeRO-1 shard update (declarations: include/yoco_z1.h).
+//
+// Layout and scheduling
+//   * Every multi-tensor kernel walks one device-resident table of rows (g, p, m, v, p16, n) cut into fixed
+//     chunks of kChunk elements; row r owns the global chunk range [chunk0_r, chunk0_r + ceil(n_r / kChunk)).
+//   * Persistent grid: workgroup b takes chunks b, b + G, b + 2G, ... (G = grid size).  A workgroup's chunk index
+//     only grows, so its row index only advances (a few scalar loads per chunk at most).
+//   * Inside a full chunk each lane streams kGroups float4 groups per array; the groups of one wave are
+//     consecutive 16-byte slots, so every load/store instruction of a wave covers 1 KiB (fp32) or 512 B (bf16)
+//     contiguous bytes.  The last, partial chunk of a row (and any row whose pointers are not aligned for the
+//     vector path) runs an element-wise loop.
+//   * The norm uses the same table and a FIXED grid (Z1_NORM_PARTIALS workgroups), FP64 accumulation of the exact
+//     squares per lane, a wave64 xor-butterfly and a fixed-order LDS stage: its bits do not depend on timing, on
+//     the device's CU count or on the run.
+//   * No atomics anywhere; nothing but vector memory instructions write memory.
+//
+// Numerics follow the header: one rounding per fp32 operation, explicit FMAs where the reference has them,
+// correctly rounded division and square root (built with -fhip-fp32-correctly-rounded-divide-sqrt, no fast math,
+// fp32 denormals kept, no contraction).
+#include <hip/hip_runtime.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <mutex>
+#include <new>
+#include <vector>
+
+#include "yoco_z1.h"
+
+#pragma clang fp contract(off)
+
+#ifndef Z1_GROUPS
+#define Z1_GROUPS 4              // float4 groups per lane per chunk
+#endif
+#ifndef Z1_NT
+#define Z1_NT 1                  // nontemporal (streaming) hints on the big streams
+#endif
+
+namespace {
+
+constexpr int kThreads = 256;                                 // 4 wave64 per workgroup
+constexpr int kVec = 4;                                       // fp32 lanes of one 128-bit access
+constexpr int kGroups = Z1_GROUPS;
+constexpr int64_t kChunk = (int64_t)kThreads * kVec * kGroups;   // elements per chunk
+constexpr int kMaxDevices = 64;
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+
+// Device copy of one table row plus its schedule.  64 bytes: one scalar load brings a whole row.
+struct Row {
+    const void* g;
+    float* p;
+    float* m;
+    float* v;
+    uint16_t* p16;
+    int64_t n;
+    int64_t chunk0;
+    int32_t vec;        // bit 0: g aligned for the vector path; bit 1: p, m, v, p16 aligned as well
+    int32_t pad;
+};
+static_assert(sizeof(Row) == 64, "row layout");
+
+enum { kVecG = 1, kVecAll = 2 };
+
+struct AdamK {
+    float lr, b1, b2, eps, bc1, bc2, wd, omb1, omb2;
+};
+
+// Streams go through the global address space (global_load/global_store, not flat): the pointers come out of a
+// table in memory, so the compiler cannot infer the address space by itself.
+#define Z1_GLOBAL __attribute__((address_space(1)))
+
+template <typename T>
+__device__ __forceinline__ T ld(const T* p) {
+    const Z1_GLOBAL T* gp = (const Z1_GLOBAL T*)p;
+#if Z1_NT
+    return __builtin_nontemporal_load(gp);
+#else
+    return *gp;
+#endif
+}
+
+template <typename T>
+__device__ __forceinline__ void st(T* p, T x) {
+    Z1_GLOBAL T* gp = (Z1_GLOBAL T*)p;
+#if Z1_NT
+    __builtin_nontemporal_store(x, gp);
+#else
+    *gp = x;
+#endif
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round to nearest even; NaN -> 0x7FC0.
+__device__ __forceinline__ uint32_t f32_to_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    return ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc0u : r;
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) { return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16); }
+
+template <int MODE>
+__device__ __forceinline__ void adam_elem(float g, float& p, float& m, float& v, const AdamK& k) {
+    if (MODE == 0) g = __builtin_fmaf(k.wd, p, g);
+    m = __builtin_fmaf(k.b1, m, k.omb1 * g);
+    const float t = k.omb2 * g;
+    v = __builtin_fmaf(k.b2, v, t * g);
+    const float mh = m / k.bc1;
+    const float vh = v / k.bc2;
+    const float den = __builtin_sqrtf(vh) + k.eps;
+    float upd = mh / den;
+    if (MODE == 1) upd = __builtin_fmaf(k.wd, p, upd);
+    p = __builtin_fmaf(-k.lr, upd, p);
+}
+
+// Advances `t` to the row that owns chunk c (c only grows within a workgroup).
+__device__ __forceinline__ int row_of(const Row* __restrict__ rows, int nrows, int t, int64_t c) {
+    while (t + 1 < nrows && rows[t + 1].chunk0 <= c) ++t;
+    return t;
+}
+
+// ------------------------------------------------------------------------------------------------ Adam + BF16
+template <int GDT>
+__device__ __forceinline__ f4 load_g4(const void* g, int64_t i) {
+    if (GDT == Z1_F32) return ld(reinterpret_cast<const f4*>(static_cast<const float*>(g) + i));
+    const u2 h = ld(reinterpret_cast<const u2*>(static_cast<const uint16_t*>(g) + i));
+    return f4{bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y)};
+}
+
+template <int GDT>
+__device__ __forceinline__ float load_g1(const void* g, int64_t i) {
+    if (GDT == Z1_F32) return static_cast<const float*>(g)[i];
+    return bf16_to_f32(static_cast<const uint16_t*>(g)[i]);
+}
+
+template <int GDT, int MODE>
+__global__ __launch_bounds__(kThreads) void adam_cast_kernel(const Row* __restrict__ rows, int nrows,
+                                                             int64_t nchunks, const float* __restrict__ factor,
+                                                             AdamK k) {
+    const float f = factor ? *factor : 1.0f;
+    const int tid = threadIdx.x;
+    int t = 0;
+    for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+        t = row_of(rows, nrows, t, c);
+        const Row r = rows[t];
+        const int64_t base = (c - r.chunk0) * kChunk;
+        const int64_t rem = r.n - base;
+        if (rem >= kChunk && (r.vec & kVecAll)) {
+            f4 g[kGroups], p[kGroups], m[kGroups], v[kGroups];
+#pragma unroll
+            for (int u = 0; u < kGroups; ++u) {
+                const int64_t i = base + (int64_t)(u * kThreads + tid) * kVec;
+                g[u] = load_g4<GDT>(r.g, i);
+                p[u] = ld(reinterpret_cast<const f4*>(r.p + i));
+                m[u] = ld(reinterpret_cast<const f4*>(r.m + i));
+                v[u] = ld(reinterpret_cast<const f4*>(r.v + i));
+            }
+#pragma unroll
+            for (int u = 0; u < kGroups; ++u) {
+#pragma unroll
+                for (int j = 0; j < kVec; ++j) {
+                    float pj = p[u][j], mj = m[u][j], vj = v[u][j];
+                    adam_elem<MODE>(g[u][j] * f, pj, mj, vj, k);
+                    p[u][j] = pj;
+                    m[u][j] = mj;
+                    v[u][j] = vj;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kGroups; ++u) {
+                const int64_t i = base + (int64_t)(u * kThreads + tid) * kVec;
+                st(reinterpret_cast<f4*>(r.p + i), p[u]);
+                st(reinterpret_cast<f4*>(r.m + i), m[u]);
+                st(reinterpret_cast<f4*>(r.v + i), v[u]);
+                if (r.p16) {
+                    const u2 h = u2{pack_bf16(p[u][0], p[u][1]), pack_bf16(p[u][2], p[u][3])};
+                    st(reinterpret_cast<u2*>(r.p16 + i), h);
+                }
+            }
+        } else {
+            const int64_t cnt = rem < kChunk ? rem : kChunk;
+            for (int64_t i = base + tid; i < base + cnt; i += kThreads) {
+                float pj = r.p[i], mj = r.m[i], vj = r.v[i];
+                adam_elem<MODE>(load_g1<GDT>(r.g, i) * f, pj, mj, vj, k);
+                r.p[i] = pj;
+                r.m[i] = mj;
+                r.v[i] = vj;
+                if (r.p16) r.p16[i] = (uint16_t)f32_to_bf16(pj);
+            }
+        }
+    }
+}
+
+// -------------------------------------------------------------------------------------- deterministic norm
+// Sum over the workgroup, result valid in thread 0: xor butterfly inside each wave64 (a + b == b + a exactly, so
+// every lane ends with the same bits), then the four wave sums in wave order.
+__device__ __forceinline__ double block_sum(double x, double* lds) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
+    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = x;
+    __syncthreads();
+    double s = 0.0;
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int w = 0; w < kThreads / 64; ++w) s += lds[w];
+    }
+    return s;
+}
+
+__device__ __forceinline__ double sq64(float x) {
+    const double d = (double)x;
+    return d * d;                      // exact: 24-bit significand squared
+}
+
+template <int GDT>
+__global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__ rows, int nrows, int64_t nchunks,
+                                                         double* __restrict__ partials) {
+    __shared__ double lds[kThreads / 64];
+    const int tid = threadIdx.x;
+    double acc = 0.0;
+    int t = 0;
+    for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
+        t = row_of(rows, nrows, t, c);
+        const Row r = rows[t];
+        const int64_t base = (c - r.chunk0) * kChunk;
+        const int64_t rem = r.n - base;
+        if (rem >= kChunk && (r.vec & kVecG)) {
+            f4 g[kGroups];
+#pragma unroll
+            for (int u = 0; u < kGroups; ++u) g[u] = load_g4<GDT>(r.g, base + (int64_t)(u * kThreads + tid) * kVec);
+#pragma unroll
+            for (int u = 0; u < kGroups; ++u) {
+#pragma unroll
+                for (int j = 0; j < kVec; ++j) acc += sq64(g[u][j]);
+            }
+        } else {
+            const int64_t cnt = rem < kChunk ? rem : kChunk;
+            for (int64_t i = base + tid; i < base + cnt; i += kThreads) acc += sq64(load_g1<GDT>(r.g, i));
+        }
+    }
+    const double s = block_sum(acc, lds);
+    if (tid == 0) partials[blockIdx.x] = s;
+}
+
+// zero1_fast.py:150-160 scalar chain, one owner.
+__device__ __forceinline__ void clip_chain(float norm, float fac, float* grad_norm_out, float* factor_out,
+                                           float max_norm) {
+    const float gn = fac * norm;
+    if (grad_norm_out) *grad_norm_out = gn;
+    float f = fac;
+    if (max_norm > 0.0f) {
+        const float t = gn + 1e-6f;
+        float coef = (1.0f / t) * max_norm;
+        coef = (coef > 1.0f) ? 1.0f : coef;           // clamp(max=1), NaN stays NaN
+        f = fac * coef;
+    }
+    if (factor_out) *factor_out = f;
+}
+
+__global__ __launch_bounds__(kThreads) void norm_clip_kernel(const double* __restrict__ partials,
+                                                             const float* factor_in, float factor_value,
+                                                             float* norm_out, float* grad_norm_out, float* factor_out,
+                                                             float max_norm) {
+    __shared__ double lds[kThreads / 64];
+    double s = 0.0;
+    for (int i = threadIdx.x; i < Z1_NORM_PARTIALS; i += kThreads) s += partials[i];
+    const double tot = block_sum(s, lds);
+    if (threadIdx.x == 0) {
+        const float nr = (float)__builtin_sqrt(tot);  // the fp32 norm clip_grad_norm_ returns
+        const float sq = nr * nr;                      // .float() ** 2 (all_reduce over one owner: identity)
+        const float norm = __builtin_sqrtf(sq);
+        if (norm_out) *norm_out = nr;
+        clip_chain(norm, factor_in ? *factor_in : factor_value, grad_norm_out, factor_out, max_norm);
+    }
+}
+
+__global__ void clip_factor_kernel(const float* __restrict__ norm, const float* factor_in, float factor_value,
+                                   float* grad_norm_out, float* factor_out, float max_norm) {
+    if (threadIdx.x == 0) clip_chain(*norm, factor_in ? *factor_in : factor_value, grad_norm_out, factor_out, max_norm);
+}
+
+// ---------------------------------------------------------------------------------------------- owner sum
+struct Srcs {
+    const uint16_t* p[Z1_MAX_WORLD];
+};
+
+// OUT may alias one source: every element is read before the same lane writes it.
+template <int MAXW>
+__global__ __launch_bounds__(kThreads) void owner_sum_kernel(Srcs s, int world, int64_t n, float scale, uint16_t* out,
+                                                             float* out_sum, double* partials, int vec) {
+    __shared__ double lds[kThreads / 64];
+    const int64_t nthreads = (int64_t)gridDim.x * kThreads;
+    const int64_t gtid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    double acc2 = 0.0;
+    int64_t tail0 = 0;
+    if (vec) {
+        const int64_t ng = n / 8;
+        tail0 = ng * 8;
+        for (int64_t gi = gtid; gi < ng; gi += nthreads) {
+            u4 x[MAXW];
+#pragma unroll
+            for (int k = 0; k < MAXW; ++k)
+                if (k < world) x[k] = ld(reinterpret_cast<const u4*>(s.p[k]) + gi);
+            float a[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) a[j] = 0.0f;
+#pragma unroll
+            for (int k = 0; k < MAXW; ++k) {
+                if (k < world) {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        a[2 * w] = a[2 * w] + bf16_lo(x[k][w]);
+                        a[2 * w + 1] = a[2 * w + 1] + bf16_hi(x[k][w]);
+                    }
+                }
+            }
+            u4 o;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) o[w] = pack_bf16(a[2 * w] * scale, a[2 * w + 1] * scale);
+            st(reinterpret_cast<u4*>(out) + gi, o);
+            if (out_sum) {
+                st(reinterpret_cast<f4*>(out_sum) + 2 * gi, f4{a[0], a[1], a[2], a[3]});
+                st(reinterpret_cast<f4*>(out_sum) + 2 * gi + 1, f4{a[4], a[5], a[6], a[7]});
+            }
+            if (partials) {
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    acc2 += sq64(bf16_lo(o[w]));
+                    acc2 += sq64(bf16_hi(o[w]));
+                }
+            }
+        }
+    }
+    for (int64_t e = tail0 + gtid; e < n; e += nthreads) {
+        float a = 0.0f;
+        for (int k = 0; k < world; ++k) a = a + bf16_to_f32(s.p[k][e]);
+        const uint32_t o = f32_to_bf16(a * scale);
+        out[e] = (uint16_t)o;
+        if (out_sum) out_sum[e] = a;
+        if (partials) acc2 += sq64(bf16_to_f32((uint16_t)o));
+    }
+    if (partials) {
+        const double t = block_sum(acc2, lds);
+        if (threadIdx.x == 0) partials[blockIdx.x] = t;
+    }
+}
+
+// ------------------------------------------------------------------------------------- scale / cast passes
+__global__ __launch_bounds__(kThreads) void scale_up_kernel(const uint16_t* __restrict__ g16, float* __restrict__ g32,
+                                                            const float* __restrict__ factor, int64_t n, int vec) {
+    const float f = *factor;
+    const int64_t nthreads = (int64_t)gridDim.x * kThreads;
+    const int64_t gtid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    int64_t tail0 = 0;
+    if (vec) {
+        const int64_t ng = n / 8;
+        tail0 = ng * 8;
+        for (int64_t gi = gtid; gi < ng; gi += nthreads) {
+            const u4 h = ld(reinterpret_cast<const u4*>(g16) + gi);
+            st(reinterpret_cast<f4*>(g32) + 2 * gi, f4{bf16_lo(h.x) * f, bf16_hi(h.x) * f, bf16_lo(h.y) * f,
+                                                        bf16_hi(h.y) * f});
+            st(reinterpret_cast<f4*>(g32) + 2 * gi + 1, f4{bf16_lo(h.z) * f, bf16_hi(h.z) * f, bf16_lo(h.w) * f,
+                                                            bf16_hi(h.w) * f});
+        }
+    }
+    for (int64_t e = tail0 + gtid; e < n; e += nthreads) g32[e] = bf16_to_f32(g16[e]) * f;
+}
+
+__global__ __launch_bounds__(kThreads) void cast_bf16_kernel(const float* __restrict__ p32, uint16_t* __restrict__ p16,
+                                                             int64_t n, int vec) {
+    const int64_t nthreads = (int64_t)gridDim.x * kThreads;
+    const int64_t gtid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+    int64_t tail0 = 0;
+    if (vec) {
+        const int64_t ng = n / 8;
+        tail0 = ng * 8;
+        for (int64_t gi = gtid; gi < ng; gi += nthreads) {
+            const f4 a = ld(reinterpret_cast<const f4*>(p32) + 2 * gi);
+            const f4 b = ld(reinterpret_cast<const f4*>(p32) + 2 * gi + 1);
+            st(reinterpret_cast<u4*>(p16) + gi,
+               u4{pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y), pack_bf16(b.z, b.w)});
+        }
+    }
+    for (int64_t e = tail0 + gtid; e < n; e += nthreads) p16[e] = (uint16_t)f32_to_bf16(p32[e]);
+}
+
+// -------------------------------------------------------------------------------------------- host helpers
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+struct DevInfo {
+    int cus = 0;
+    int adam_blocks[2][2] = {{0, 0}, {0, 0}};   // [gdt][mode] resident workgroups per CU
+};
+
+std::mutex g_mu;
+DevInfo g_dev[kMaxDevices];
+
+int current_device(int* dev) {
+    hipError_t e = hipGetDevice(dev);
+    if (e != hipSuccess) return (int)e;
+    if (*dev < 0 || *dev >= kMaxDevices) return Z1_E_DEVICE;
+    return Z1_OK;
+}
+
+int cu_count(int dev, int* cus) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_dev[dev].cus == 0) {
+        int v = 0;
+        hipError_t e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
+        if (e != hipSuccess) return (int)e;
+        g_dev[dev].cus = v > 0 ? v : 1;
+    }
+    *cus = g_dev[dev].cus;
+    return Z1_OK;
+}
+
+template <int GDT, int MODE>
+int adam_grid(int dev, int64_t nchunks, int* grid) {
+    int cus = 0;
+    int rc = cu_count(dev, &cus);
+    if (rc) return rc;
+    int per = 0;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        per = g_dev[dev].adam_blocks[GDT][MODE];
+    }
+    if (per == 0) {
+        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per, reinterpret_cast<const void*>(&adam_cast_kernel<GDT, MODE>), kThreads, 0);
+        if (e != hipSuccess) return (int)e;
+        if (per < 1) per = 1;
+        std::lock_guard<std::mutex> lk(g_mu);
+        g_dev[dev].adam_blocks[GDT][MODE] = per;
+    }
+    int64_t g = (int64_t)cus * per;
+    if (g > nchunks) g = nchunks;
+    *grid = (int)(g < 1 ? 1 : g);
+    return Z1_OK;
+}
+
+int stream_grid(int dev, int64_t groups, int* grid) {
+    int cus = 0;
+    int rc = cu_count(dev, &cus);
+    if (rc) return rc;
+    int64_t want = (groups + kThreads - 1) / kThreads;
+    int64_t cap = (int64_t)cus * 8;
+    if (want > cap) want = cap;
+    *grid = (int)(want < 1 ? 1 : want);
+    return Z1_OK;
+}
+
+inline int launch_status() {
+    hipError_t e = hipGetLastError();
+    return e == hipSuccess ? Z1_OK : (int)e;
+}
+
+}  // namespace
+
+struct z1_table {
+    Row* rows;            // device
+    int nrows;
+    int g_dtype;
+    int device;
+    int has_pmv;          // every row has p, m and v
+    int64_t numel;
+    int64_t nchunks;
+};
+
+extern "C" {
+
+int z1_table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table** out) {
+    if (!out) return Z1_E_NULL;
+    *out = nullptr;
+    if (nrows < 0) return Z1_E_SIZE;
+    if (nrows > 0 && !rows) return Z1_E_NULL;
+    if (g_dtype != Z1_F32 && g_dtype != Z1_BF16) return Z1_E_DTYPE;
+    const uintptr_t galign = g_dtype == Z1_F32 ? 16 : 8;
+    std::vector<Row> h;
+    h.reserve(nrows);
+    int64_t chunks = 0, numel = 0;
+    int has_pmv = 1;
+    for (int i = 0; i < nrows; ++i) {
+        const z1_tensor& t = rows[i];
+        if (t.n < 0) return Z1_E_SIZE;
+        if (t.n == 0) continue;
+        if (!t.g) return Z1_E_NULL;
+        Row r;
+        r.g = t.g;
+        r.p = t.p;
+        r.m = t.m;
+        r.v = t.v;
+        r.p16 = t.p16;
+        r.n = t.n;
+        r.chunk0 = chunks;
+        r.vec = 0;
+        r.pad = 0;
+        if (aligned(t.g, galign)) {
+            r.vec |= kVecG;
+            if (aligned(t.p, 16) && aligned(t.m, 16) && aligned(t.v, 16) && (!t.p16 || aligned(t.p16, 8)))
+                r.vec |= kVecAll;
+        }
+        if (!t.p || !t.m || !t.v) has_pmv = 0;
+        chunks += (t.n + kChunk - 1) / kChunk;
+        numel += t.n;
+        h.push_back(r);
+    }
+    int dev = 0;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    z1_table* tb = new (std::nothrow) z1_table();
+    if (!tb) return (int)hipErrorOutOfMemory;
+    tb->nrows = (int)h.size();
+    tb->g_dtype = g_dtype;
+    tb->device = dev;
+    tb->has_pmv = has_pmv;
+    tb->numel = numel;
+    tb->nchunks = chunks;
+    tb->rows = nullptr;
+    const size_t bytes = sizeof(Row) * (h.empty() ? 1 : h.size());
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&tb->rows), bytes);
+    if (e != hipSuccess) {
+        delete tb;
+        return (int)e;
+    }
+    if (!h.empty()) {
+        e = hipMemcpy(tb->rows, h.data(), sizeof(Row) * h.size(), hipMemcpyHostToDevice);
+        if (e != hipSuccess) {
+            (void)hipFree(tb->rows);
+            delete tb;
+            return (int)e;
+        }
+    }
+    *out = tb;
+    return Z1_OK;
+}
+
+int z1_table_destroy(z1_table* table) {
+    if (!table) return Z1_OK;
+    int prev = 0;
+    hipError_t e = hipGetDevice(&prev);
+    if (e == hipSuccess && prev != table->device) e = hipSetDevice(table->device);
+    if (e == hipSuccess) e = hipFree(table->rows);
+    if (prev != table->device) (void)hipSetDevice(prev);
+    delete table;
+    return e == hipSuccess ? Z1_OK : (int)e;
+}
+
+int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* nrows) {
+    if (!table) return Z1_E_NULL;
+    if (numel) *numel = table->numel;
+    if (nchunks) *nchunks = table->nchunks;
+    if (nrows) *nrows = table->nrows;
+    return Z1_OK;
+}
+
+static int check_table_device(const z1_table* table, int* dev) {
+    int rc = current_device(dev);
+    if (rc) return rc;
+    return *dev == table->device ? Z1_OK : Z1_E_DEVICE;
+}
+
+int z1_grad_sumsq(const z1_table* table, double* partials, void* stream) {
+    if (!table || !partials) return Z1_E_NULL;
+    int dev = 0;
+    int rc = check_table_device(table, &dev);
+    if (rc) return rc;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (table->g_dtype == Z1_F32)
+        hipLaunchKernelGGL(sumsq_kernel<Z1_F32>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
+                           table->nrows, table->nchunks, partials);
+    else
+        hipLaunchKernelGGL(sumsq_kernel<Z1_BF16>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
+                           table->nrows, table->nchunks, partials);
+    return launch_status();
+}
+
+int z1_norm_clip(const double* partials, const float* factor_in, float factor_value, float* norm_out,
+                 float* grad_norm_out, float* factor_out, float max_norm, void* stream) {
+    if (!partials) return Z1_E_NULL;
+    hipLaunchKernelGGL(norm_clip_kernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), partials,
+                       factor_in, factor_value, norm_out, grad_norm_out, factor_out, max_norm);
+    return launch_status();
+}
+
+int z1_clip_factor(const float* norm, const float* factor_in, float factor_value, float* grad_norm_out,
+                   float* factor_out, float max_norm, void* stream) {
+    if (!norm) return Z1_E_NULL;
+    hipLaunchKernelGGL(clip_factor_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream), norm, factor_in,
+                       factor_value, grad_norm_out, factor_out, max_norm);
+    return launch_status();
+}
+
+int z1_adam_cast(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
+                 float bc1, float bc2, float weight_decay, int mode, void* stream) {
+    if (!table) return Z1_E_NULL;
+    if (mode != 0 && mode != 1) return Z1_E_MODE;
+    if (!table->has_pmv) return Z1_E_NULL;
+    int dev = 0;
+    int rc = check_table_device(table, &dev);
+    if (rc) return rc;
+    if (table->nchunks == 0) return Z1_OK;
+    AdamK k;
+    k.lr = lr;
+    k.b1 = beta1;
+    k.b2 = beta2;
+    k.eps = eps;
+    k.bc1 = bc1;
+    k.bc2 = bc2;
+    k.wd = weight_decay;
+    k.omb1 = 1.0f - beta1;
+    k.omb2 = 1.0f - beta2;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int grid = 0;
+#define Z1_LAUNCH_ADAM(GDT, MODE)                                                                            \
+    do {                                                                                                     \
+        rc = adam_grid<GDT, MODE>(dev, table->nchunks, &grid);                                              \
+        if (rc) return rc;                                                                                   \
+        hipLaunchKernelGGL((adam_cast_kernel<GDT, MODE>), dim3(grid), dim3(kThreads), 0, s, table->rows,    \
+                           table->nrows, table->nchunks, factor, k);                                         \
+    } while (0)
+    if (table->g_dtype == Z1_F32) {
+        if (mode == 1) Z1_LAUNCH_ADAM(Z1_F32, 1);
+        else Z1_LAUNCH_ADAM(Z1_F32, 0);
+    } else {
+        if (mode == 1) Z1_LAUNCH_ADAM(Z1_BF16, 1);
+        else Z1_LAUNCH_ADAM(Z1_BF16, 0);
+    }
+#undef Z1_LAUNCH_ADAM
+    return launch_status();
+}
+
+int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                      float* out_sum, double* sumsq_partials, void* stream) {
+    if (!contrib || !out_avg) return Z1_E_NULL;
+    if (world < 1 || world > Z1_MAX_WORLD) return Z1_E_WORLD;
+    if (n < 0) return Z1_E_SIZE;
+    Srcs srcs;
+    memset(&srcs, 0, sizeof(srcs));
+    int vec = aligned(out_avg, 16) && (!out_sum || aligned(out_sum, 16));
+    for (int k = 0; k < world; ++k) {
+        if (!contrib[k]) return Z1_E_NULL;
+        srcs.p[k] = contrib[k];
+        if (!aligned(contrib[k], 16)) vec = 0;
+    }
+    if (n == 0 && !sumsq_partials) return Z1_OK;
+    int dev = 0;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    int grid = Z1_NORM_PARTIALS;             // fixed when the norm partials are fused (their order)
+    if (!sumsq_partials) {
+        rc = stream_grid(dev, (n + 7) / 8, &grid);
+        if (rc) return rc;
+    }
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (world <= 8)
+        hipLaunchKernelGGL(owner_sum_kernel<8>, dim3(grid), dim3(kThreads), 0, s, srcs, world, n, scale, out_avg,
+                           out_sum, sumsq_partials, vec);
+    else
+        hipLaunchKernelGGL(owner_sum_kernel<Z1_MAX_WORLD>, dim3(grid), dim3(kThreads), 0, s, srcs, world, n, scale,
+                           out_avg, out_sum, sumsq_partials, vec);
+    return launch_status();
+}
+
+int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n, void* stream) {
+    if (!g16 || !g32 || !factor) return Z1_E_NULL;
+    if (n < 0) return Z1_E_SIZE;
+    if (n == 0) return Z1_OK;
+    int dev = 0, grid = 0;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    rc = stream_grid(dev, (n + 7) / 8, &grid);
+    if (rc) return rc;
+    const int vec = aligned(g16, 16) && aligned(g32, 16);
+    hipLaunchKernelGGL(scale_up_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), g16, g32,
+                       factor, n, vec);
+    return launch_status();
+}
+
+int z1_cast_bf16(const float* p32, uint16_t* p16, int64_t n, void* stream) {
+    if (!p32 || !p16) return Z1_E_NULL;
+    if (n < 0) return Z1_E_SIZE;
+    if (n == 0) return Z1_OK;
+    int dev = 0, grid = 0;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    rc = stream_grid(dev, (n + 7) / 8, &grid);
+    if (rc) return rc;
+    const int vec = aligned(p32, 16) && aligned(p16, 16);
+    hipLaunchKernelGGL(cast_bf16_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p32, p16, n,
+                       vec);
+    return launch_status();
+}
+
+const char* z1_strerror(int code) {
+    switch (code) {
+        case Z1_OK: return "ok";
+        case Z1_E_NULL: return "a required pointer is NULL";
+        case Z1_E_SIZE: return "invalid element count";
+        case Z1_E_DTYPE: return "unknown gradient dtype";
+        case Z1_E_WORLD: return "world outside 1..Z1_MAX_WORLD";
+        case Z1_E_MODE: return "Adam mode must be 0 or 1";
+        case Z1_E_WORKSPACE: return "workspace too small";
+        case Z1_E_DEVICE: return "table used on another device than it was created on";
+        default: break;
+    }
+    if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));
+    return "unknown error";
+}
+
+}  // extern "C"

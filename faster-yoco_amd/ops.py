@@ -1,0 +1,229 @@
+"""Thin torch-tensor wrappers over the C ABI.  Every call enqueues on torch's current stream of the tensors'
+device, performs no host synchronisation and no allocation (tables are built once, at set-up)."""
+import ctypes
+import math
+from collections import OrderedDict
+
+import torch
+
+from ._lib import (Z1_BF16, Z1_F32, Z1_MAX_WORLD, Z1_NORM_PARTIALS, Z1Tensor, check, lib, ptr, require_gpu,
+                   stream_handle)
+
+_GDTYPE = {torch.float32: Z1_F32, torch.bfloat16: Z1_BF16}
+
+
+def f32(x):
+    """Round a Python number to fp32 as a Triton / ctypes fp32 scalar argument receives it (RNE)."""
+    return ctypes.c_float(float(x)).value
+
+
+class Table:
+    """Device-resident tensor-offset table over (g, p, m, v, p16) rows.  Holds only addresses: the caller keeps
+    the tensors alive and unmoved while the table is used (as the reference's dest map of data_ptrs does,
+    yoco/tasks/fused_adam_cast.py:49-50)."""
+
+    def __init__(self, rows, device):
+        """rows: sequence of (g, p, m, v, p16, n); tensors or None (p/m/v/p16), all on `device`."""
+        self.device = torch.device(device)
+        gd = None
+        arr = (Z1Tensor * max(1, len(rows)))()
+        for i, (g, p, m, v, p16, n) in enumerate(rows):
+            if g is None:
+                raise RuntimeError('yoco_z1: a table row has no gradient')
+            code = _GDTYPE.get(g.dtype)
+            if code is None or (gd is not None and code != gd):
+                raise RuntimeError(f'yoco_z1: gradients must all be fp32 or all bf16, got {g.dtype}')
+            gd = code
+            for t in (g, p, m, v, p16):
+                if t is not None:
+                    require_gpu(t, 'yoco_z1')
+                    if t.device != self.device:
+                        raise RuntimeError('yoco_z1: table tensors on different devices')
+            arr[i] = Z1Tensor(g.data_ptr(), p.data_ptr() if p is not None else None,
+                              m.data_ptr() if m is not None else None, v.data_ptr() if v is not None else None,
+                              p16.data_ptr() if p16 is not None else None, int(n))
+        self.g_dtype = Z1_F32 if gd is None else gd
+        self.nrows = len(rows)
+        h = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            check(lib().z1_table_create(arr, len(rows), self.g_dtype, ctypes.byref(h)), 'z1_table_create')
+        self._h = h
+        numel, nch, nr = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int()
+        check(lib().z1_table_info(h, ctypes.byref(numel), ctypes.byref(nch), ctypes.byref(nr)), 'z1_table_info')
+        self.numel, self.nchunks = numel.value, nch.value
+
+    @property
+    def handle(self):
+        return self._h
+
+    def close(self):
+        h, self._h = getattr(self, '_h', None), None
+        if h is not None and h.value:
+            try:
+                with torch.cuda.device(self.device):
+                    lib().z1_table_destroy(h)
+            except Exception:           # interpreter shutdown: the process frees device memory anyway
+                pass
+
+    def __del__(self):
+        self.close()
+
+
+class TableCache:
+    """Tables keyed by the addresses and sizes they describe (bounded, least recently used evicted).  A hit
+    means the same addresses and sizes, so the cached schedule is valid for whichever tensors live there now."""
+
+    def __init__(self, capacity=8):
+        self.capacity = capacity
+        self._d = OrderedDict()
+
+    def get(self, rows, device):
+        key = (str(device),) + tuple((g.data_ptr(), g.dtype, p.data_ptr() if p is not None else 0,
+                                      m.data_ptr() if m is not None else 0, v.data_ptr() if v is not None else 0,
+                                      p16.data_ptr() if p16 is not None else 0, int(n))
+                                     for g, p, m, v, p16, n in rows)
+        t = self._d.get(key)
+        if t is None:
+            t = Table(rows, device)
+            self._d[key] = t
+            while len(self._d) > self.capacity:
+                self._d.popitem(last=False)[1].close()
+        else:
+            self._d.move_to_end(key)
+        return t
+
+    def clear(self):
+        for t in self._d.values():
+            t.close()
+        self._d.clear()
+
+
+def norm_workspace(device):
+    """Workspace of the norm partials (Z1_NORM_PARTIALS doubles)."""
+    return torch.empty(Z1_NORM_PARTIALS, dtype=torch.float64, device=device)
+
+
+def grad_sumsq(table, partials):
+    require_gpu(partials, 'grad_sumsq')
+    if partials.dtype != torch.float64 or partials.numel() < Z1_NORM_PARTIALS:
+        raise RuntimeError('yoco_z1: norm workspace must hold Z1_NORM_PARTIALS float64')
+    with torch.cuda.device(table.device):
+        check(lib().z1_grad_sumsq(table.handle, ptr(partials), stream_handle(table.device)), 'z1_grad_sumsq')
+
+
+def _scalar(t, what):
+    if t is None:
+        return None
+    require_gpu(t, what)
+    if t.dtype != torch.float32 or t.numel() != 1:
+        raise RuntimeError(f'{what}: expected a 1-element fp32 device tensor')
+    return ptr(t)
+
+
+def _factor_args(factor):
+    """(device pointer or None, host value) for a fairseq-style factor: a Python number or a 1-element fp32
+    device tensor."""
+    if torch.is_tensor(factor):
+        return _scalar(factor, 'factor'), 1.0
+    return None, f32(1.0 if factor is None else factor)
+
+
+def norm_clip(partials, factor=1.0, norm_out=None, grad_norm_out=None, factor_out=None, max_norm=0.0):
+    """Final fixed-order reduction + the clip chain (include/yoco_z1.h).  factor: Python number or 1-element fp32
+    device tensor (read); factor_out (nullable, may be `factor`) receives the clipped factor."""
+    require_gpu(partials, 'norm_clip')
+    dev = partials.device
+    fin, fval = _factor_args(factor)
+    with torch.cuda.device(dev):
+        check(lib().z1_norm_clip(ptr(partials), fin, fval, _scalar(norm_out, 'norm_clip'),
+                                 _scalar(grad_norm_out, 'norm_clip'), _scalar(factor_out, 'norm_clip'), f32(max_norm),
+                                 stream_handle(dev)), 'z1_norm_clip')
+
+
+def clip_factor(norm, factor=1.0, grad_norm_out=None, factor_out=None, max_norm=0.0):
+    """The clip chain entered at `norm` (1-element fp32 device tensor)."""
+    dev = norm.device
+    fin, fval = _factor_args(factor)
+    with torch.cuda.device(dev):
+        check(lib().z1_clip_factor(_scalar(norm, 'clip_factor'), fin, fval, _scalar(grad_norm_out, 'clip_factor'),
+                                   _scalar(factor_out, 'clip_factor'), f32(max_norm), stream_handle(dev)),
+              'z1_clip_factor')
+
+
+def bias_corrections(beta1, beta2, step, bias_correction=1):
+    """yoco/tasks/fused_adam_cast.py:58-60: 1 - beta**step in double, rounded once to fp32."""
+    if bias_correction == 1:
+        return f32(1.0 - math.pow(beta1, step)), f32(1.0 - math.pow(beta2, step))
+    return 1.0, 1.0
+
+
+def adam_cast(table, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode):
+    """One persistent-grid Adam + BF16 launch over the table.  factor: 1-element fp32 device tensor or None."""
+    with torch.cuda.device(table.device):
+        check(lib().z1_adam_cast(table.handle, _scalar(factor, 'adam_cast'), f32(lr), f32(beta1), f32(beta2),
+                                 f32(eps), f32(bc1), f32(bc2), f32(weight_decay), int(mode),
+                                 stream_handle(table.device)), 'z1_adam_cast')
+
+
+def owner_sum(contribs, out, scale, out_sum=None, partials=None):
+    """out[e] = bf16(sum_k float(contribs[k][e]) * scale), k in list order.  contribs: bf16 tensors (or raw
+    device addresses as ints) of out.numel() elements each; out may be one of them."""
+    require_gpu(out, 'owner_sum')
+    if out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise RuntimeError('yoco_z1: owner_sum output must be a contiguous bf16 tensor')
+    world = len(contribs)
+    if not 1 <= world <= Z1_MAX_WORLD:
+        raise RuntimeError(f'yoco_z1: owner_sum takes 1..{Z1_MAX_WORLD} contributions, got {world}')
+    addrs = []
+    for c in contribs:
+        if isinstance(c, int):
+            addrs.append(c)
+            continue
+        require_gpu(c, 'owner_sum')
+        if c.dtype != torch.bfloat16 or not c.is_contiguous() or c.numel() != out.numel() or c.device != out.device:
+            raise RuntimeError('yoco_z1: owner_sum contributions must be contiguous bf16 tensors like out')
+        addrs.append(c.data_ptr())
+    if out_sum is not None:
+        require_gpu(out_sum, 'owner_sum')
+        if out_sum.dtype != torch.float32 or not out_sum.is_contiguous() or out_sum.numel() != out.numel():
+            raise RuntimeError('yoco_z1: owner_sum out_sum must be a contiguous fp32 tensor like out')
+    if partials is not None and (partials.dtype != torch.float64 or partials.numel() < Z1_NORM_PARTIALS):
+        raise RuntimeError('yoco_z1: norm workspace must hold Z1_NORM_PARTIALS float64')
+    arr = (ctypes.c_void_p * world)(*addrs)
+    with torch.cuda.device(out.device):
+        check(lib().z1_owner_sum_bf16(ctypes.cast(arr, ctypes.c_void_p), world, out.numel(), f32(scale), ptr(out),
+                                      ptr(out_sum), ptr(partials), stream_handle(out.device)), 'z1_owner_sum_bf16')
+
+
+def owner_sum_raw(addrs, n, out_addr, scale, device):
+    """owner_sum on raw device addresses (the reference's slot layout, yoco/models/decoder/ce_reduce.py:59-74)."""
+    arr = (ctypes.c_void_p * len(addrs))(*addrs)
+    with torch.cuda.device(device):
+        check(lib().z1_owner_sum_bf16(ctypes.cast(arr, ctypes.c_void_p), len(addrs), int(n), f32(scale),
+                                      ctypes.c_void_p(out_addr), None, None, stream_handle(device)),
+              'z1_owner_sum_bf16')
+
+
+def scale_up(g16, g32, factor):
+    """g32 = float(g16) * factor[0] (yoco/tasks/fused_adam_cast.py:84-89)."""
+    for t in (g16, g32, factor):
+        require_gpu(t, 'scale_up')
+    if g16.dtype != torch.bfloat16 or g32.dtype != torch.float32 or g16.numel() != g32.numel():
+        raise RuntimeError('yoco_z1: scale_up expects bf16 -> fp32 of equal size')
+    if not (g16.is_contiguous() and g32.is_contiguous()):
+        raise RuntimeError('yoco_z1: scale_up expects contiguous tensors')
+    with torch.cuda.device(g32.device):
+        check(lib().z1_scale_up(ptr(g16), ptr(g32), _scalar(factor.reshape(-1)[:1], 'scale_up'), g16.numel(),
+                                stream_handle(g32.device)), 'z1_scale_up')
+
+
+def cast_bf16(p32, p16):
+    """p16 = bf16(p32), round to nearest even."""
+    for t in (p32, p16):
+        require_gpu(t, 'cast_bf16')
+    if p32.dtype != torch.float32 or p16.dtype != torch.bfloat16 or p32.numel() != p16.numel():
+        raise RuntimeError('yoco_z1: cast_bf16 expects fp32 -> bf16 of equal size')
+    if not (p32.is_contiguous() and p16.is_contiguous()):
+        raise RuntimeError('yoco_z1: cast_bf16 expects contiguous tensors')
+    with torch.cuda.device(p32.device):
+        check(lib().z1_cast_bf16(ptr(p32), ptr(p16), p32.numel(), stream_handle(p32.device)), 'z1_cast_bf16')

@@ -1,0 +1,169 @@
+"""One GPU's ZeRO-1 shard as flat HBM buffers, with the FP16Optimizer-style surface the reference's trainer
+drives (``multiply_grads`` / ``clip_grad_norm`` / ``step`` / ``zero_grad``; fairseq ``_FP16OptimizerMixin`` as
+patched by yoco/tasks/zero1_fast.py:139-244, called from yoco/tasks/trainer_nosync.py:273-289).
+
+HBM layout (one allocation per stream, every tensor's slice starting on a ``align``-element boundary):
+    p    fp32 [N]   master weights            m    fp32 [N]   exp_avg
+    v    fp32 [N]   exp_avg_sq                g    fp32 or bf16 [N]   owner gradient (the reduced average)
+    p16  bf16 [N]   the parameter copy the model reads
+plus a device-resident offset table (one row per tensor) built once.  One optimizer update is three launches:
+sum of squares (fixed-order partials) -> final reduction + clip factor -> Adam + BF16 over the table.  With
+owner-side contributions (``reduce_grads``) the sum of squares is fused into the owner sum.
+"""
+import math
+
+import torch
+
+from . import ops
+
+
+def _numel(shape):
+    return int(math.prod(shape)) if len(shape) else 1
+
+
+class FlatShard:
+    """Flat buffers + offset table for a list of tensor shapes (model order)."""
+
+    def __init__(self, shapes, device, grad_dtype=torch.float32, bf16_copy=True, align=64):
+        if grad_dtype not in (torch.float32, torch.bfloat16):
+            raise RuntimeError('yoco_z1: gradients must be fp32 or bf16')
+        if align < 1 or align & (align - 1):
+            raise RuntimeError('yoco_z1: align must be a power of two')
+        self.device = torch.device(device)
+        self.shapes = [tuple(int(d) for d in s) for s in shapes]
+        self.numels = [_numel(s) for s in self.shapes]
+        self.offsets = []
+        off = 0
+        for n in self.numels:
+            off = (off + align - 1) // align * align
+            self.offsets.append(off)
+            off += n
+        self.total = off
+        self.numel = sum(self.numels)
+        dev = self.device
+        self.p = torch.zeros(self.total, dtype=torch.float32, device=dev)
+        self.m = torch.zeros(self.total, dtype=torch.float32, device=dev)
+        self.v = torch.zeros(self.total, dtype=torch.float32, device=dev)
+        self.g = torch.zeros(self.total, dtype=grad_dtype, device=dev)
+        self.p16 = torch.zeros(self.total, dtype=torch.bfloat16, device=dev) if bf16_copy else None
+        self.table = ops.Table(self._rows(), dev)
+
+    def _rows(self):
+        rows = []
+        for o, n in zip(self.offsets, self.numels):
+            sl = slice(o, o + n)
+            rows.append((self.g[sl], self.p[sl], self.m[sl], self.v[sl],
+                         None if self.p16 is None else self.p16[sl], n))
+        return rows
+
+    def views(self, buf):
+        """Per-tensor views of one flat buffer (``'p'``, ``'m'``, ``'v'``, ``'g'`` or ``'p16'``)."""
+        b = getattr(self, buf)
+        return [b[o:o + n].view(s) for o, n, s in zip(self.offsets, self.numels, self.shapes)]
+
+    def packed(self, buf):
+        """The tensors' elements of one buffer, concatenated without the alignment gaps (a copy)."""
+        b = getattr(self, buf)
+        if self.total == self.numel:
+            return b
+        return torch.cat([b[o:o + n] for o, n in zip(self.offsets, self.numels)])
+
+
+class Zero1ShardOptimizer:
+    """Mixed-precision Adam over a FlatShard with fairseq's FP16Optimizer surface.
+
+    ``_multiply_factor`` is a Python float or a 1-element fp32 device tensor, as in fairseq; the clip writes it as
+    a device tensor and ``step`` resets it to 1.0 (yoco/tasks/zero1_fast.py:158-160,193).  The step counter plays
+    FusedAdamV2's ``group['step']``; bias corrections are rounded on the host (fused_adam_cast.py:58-60).
+    """
+
+    def __init__(self, shard, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, adam_w_mode=True,
+                 bias_correction=True):
+        self.shard = shard
+        self.lr = float(lr)
+        self.betas = (float(betas[0]), float(betas[1]))
+        self.eps = float(eps)
+        self.weight_decay = float(weight_decay)
+        self.mode = 1 if adam_w_mode else 0
+        self.bias_correction = 1 if bias_correction else 0
+        self.step_count = 0
+        self._multiply_factor = 1.0
+        self._needs_sync = False
+        dev = shard.device
+        self._partials = ops.norm_workspace(dev)
+        self._factor = torch.ones(1, dtype=torch.float32, device=dev)
+        self._norm = torch.zeros(1, dtype=torch.float32, device=dev)
+        self._partials_ready = False
+
+    # -- fairseq surface -------------------------------------------------------------------------------------
+    def multiply_grads(self, c):
+        """fairseq: ``self._multiply_factor *= c`` (c a number or a device tensor)."""
+        self._multiply_factor *= c
+
+    def reduce_grads(self, contribs, scale=None):
+        """Owner-side sum of the ranks' BF16 contributions (rank order) into the shard's BF16 gradient, with the
+        norm's partials fused in (yoco/models/decoder/ce_reduce.py:59-74,178-183, + the norm of
+        zero1_fast.py:150).  contribs: flat bf16 tensors laid out like the shard's gradient buffer."""
+        if self.shard.g.dtype != torch.bfloat16:
+            raise RuntimeError('yoco_z1: reduce_grads needs a bf16 gradient shard')
+        world = len(contribs)
+        ops.owner_sum(contribs, self.shard.g, 1.0 / world if scale is None else scale, partials=self._partials)
+        # the fused partials cover the whole flat buffer; with alignment gaps the norm is taken over the table
+        self._partials_ready = self.shard.total == self.shard.numel
+
+    def clip_grad_norm(self, max_norm, aggregate_norm_fn=None):
+        """zero1_fast.py:139-162 for one owner.  Returns grad_norm as a 0-d fp32 device tensor, no host sync."""
+        if not self._partials_ready:
+            ops.grad_sumsq(self.shard.table, self._partials)
+        self._partials_ready = False
+        factor = self._multiply_factor
+        if torch.is_tensor(factor):
+            if not (factor.dtype == torch.float32 and factor.is_cuda and factor.numel() == 1):
+                factor = factor.to(device=self.shard.device, dtype=torch.float32).reshape(1)
+            out = factor                # in place, as `self._multiply_factor *= clip_coef` on a tensor
+        else:
+            out = self._factor          # a Python factor becomes a device tensor, as in the reference
+        grad_norm = torch.empty(1, dtype=torch.float32, device=self.shard.device)
+        mn = float(max_norm)
+        if aggregate_norm_fn is None:
+            ops.norm_clip(self._partials, factor=factor, norm_out=self._norm, grad_norm_out=grad_norm,
+                          factor_out=out, max_norm=mn if mn > 0.0 else 0.0)
+        else:
+            ops.norm_clip(self._partials, factor=1.0, norm_out=self._norm)
+            norm = (self._norm.float() ** 2).sqrt()
+            norm = aggregate_norm_fn(norm).reshape(1).to(torch.float32)
+            ops.clip_factor(norm, factor=factor, grad_norm_out=grad_norm, factor_out=out,
+                            max_norm=mn if mn > 0.0 else 0.0)
+        self._multiply_factor = out
+        self._needs_sync = False
+        return grad_norm.view(())
+
+    def step(self, closure=None, groups=None):
+        """Adam + BF16 over the shard with the gradient factor folded into the gradient load, then factor := 1."""
+        self.step_count += 1
+        bc1, bc2 = ops.bias_corrections(self.betas[0], self.betas[1], self.step_count, self.bias_correction)
+        factor = self._multiply_factor
+        if torch.is_tensor(factor):
+            if not (factor.dtype == torch.float32 and factor.is_cuda and factor.numel() == 1):
+                factor = factor.to(device=self.shard.device, dtype=torch.float32).reshape(1)
+        elif float(factor) == 1.0:
+            factor = None
+        else:
+            self._factor.fill_(float(factor))
+            factor = self._factor
+        ops.adam_cast(self.shard.table, factor, self.lr, self.betas[0], self.betas[1], self.eps, bc1, bc2,
+                      self.weight_decay, self.mode)
+        self._multiply_factor = 1.0
+        self._needs_sync = False
+
+    def zero_grad(self):
+        """zero1_fast.py:238-244 drops the gradients; the flat gradient is simply overwritten by the next owner
+        sum, so nothing runs here."""
+        self._needs_sync = False
+
+    # -- one full update ---------------------------------------------------------------------------------------
+    def update(self, max_norm=1.0):
+        """clip_grad_norm(max_norm) + step(): the timed optimizer update."""
+        gn = self.clip_grad_norm(max_norm)
+        self.step()
+        return gn

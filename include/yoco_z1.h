@@ -1,0 +1,114 @@
+/*
+ * yoco_z1 -- MI355X (gfx950) kernels for the owner-side, mixed-precision ZeRO-1 optimizer update of one GPU's
+ * shard: owner gradient sum, multi-tensor L2 norm + clip factor, fused Adam + BF16 copy.
+ *
+ * C ABI: plain device pointers and sizes, no framework types.  Every launch is enqueued on the caller's stream
+ * (hipStream_t passed as void*; NULL = the null stream) on the caller's current HIP device, with no host
+ * synchronisation and no allocation.  The only allocating calls are z1_table_create / z1_table_destroy (set-up).
+ *
+ * Return value: Z1_OK (0), a negative Z1_E* argument error, or a positive hipError_t from the launch.
+ * z1_strerror() turns either into text.
+ *
+ * Element semantics (the reference's, single rounding per fp32 operation, subnormals kept):
+ *   bf16(x)  = round-to-nearest-even of x to bfloat16 (NaN -> a quiet NaN)
+ *   g'       = fp32(g * factor)                                 g upcast exactly when bfloat16
+ *   m'       = fma(b1, m, fp32((1-b1)*g'))      v' = fma(b2, v, fp32(fp32((1-b2)*g')*g'))
+ *   upd      = (m'/bc1) / (sqrt(v'/bc2) + eps)  with IEEE division and square root
+ *   mode 1:  upd = fma(wd, p, upd)              mode 0: g' = fma(wd, p, g') before m', v'
+ *   p'       = fma(-lr, upd, p)                 p16 = bf16(p')
+ */
+#ifndef YOCO_Z1_H
+#define YOCO_Z1_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    Z1_OK = 0,
+    Z1_E_NULL = -1,        /* a required pointer is NULL */
+    Z1_E_SIZE = -2,        /* a negative or inconsistent element count */
+    Z1_E_DTYPE = -3,       /* unknown gradient dtype code */
+    Z1_E_WORLD = -4,       /* world outside 1..Z1_MAX_WORLD */
+    Z1_E_MODE = -5,        /* Adam mode other than 0 or 1 */
+    Z1_E_WORKSPACE = -6,   /* workspace too small */
+    Z1_E_DEVICE = -7,      /* table used on a device other than the one it was created on */
+};
+
+enum { Z1_F32 = 0, Z1_BF16 = 1 };           /* gradient dtype codes */
+
+#define Z1_MAX_WORLD 16                      /* most contributions one owner-sum call takes */
+#define Z1_NORM_PARTIALS 2048                /* doubles in the norm workspace (fixed: the reduction order) */
+
+/* One row of the tensor-offset table.  g is float* (Z1_F32) or uint16_t* bfloat16 bits (Z1_BF16).  For the norm
+ * only g and n are read; p, m, v may be NULL there.  p16 may be NULL (no BF16 copy for that tensor). */
+typedef struct z1_tensor {
+    const void* g;
+    float* p;
+    float* m;
+    float* v;
+    uint16_t* p16;
+    int64_t n;
+} z1_tensor;
+
+typedef struct z1_table z1_table;            /* opaque, device-resident table + chunk schedule */
+
+/* Builds the device copy of `rows` (plain copy of the pointers; rows with n == 0 are dropped) on the current
+ * device.  Replaces the per-call tensor-list walk of yoco/tasks/fused_adam_cast.py:62-72 and the bucket/view
+ * bookkeeping of yoco/tasks/zero1_fast.py:110-128 with one schedule built at set-up.  Allocates (hipMalloc). */
+int z1_table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table** out);
+int z1_table_destroy(z1_table* table);
+/* Total elements and chunk count of a table (host-side values). */
+int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* nrows);
+
+/* Owner-side sum (replaces the Triton kernel _sum_slots, yoco/models/decoder/ce_reduce.py:59-74, launched by
+ * CEReduce._sum :178-183):
+ *   for e in [0,n): acc = 0f; for k = 0..world-1: acc += float(contrib[k][e]); out_avg[e] = bf16(acc * scale)
+ * contrib is a HOST array of `world` device pointers (rank order); out_avg may alias one contribution (in place,
+ * as OUT does in the reference).  out_sum (nullable) receives acc in fp32.  sumsq_partials (nullable,
+ * Z1_NORM_PARTIALS doubles) receives the fused norm partials of the bf16 average for z1_norm_clip. */
+int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                      float* out_sum, double* sumsq_partials, void* stream);
+
+/* Multi-tensor sum of squares of the table's gradients (the norm of fairseq utils.clip_grad_norm_ ->
+ * apex multi_tensor_l2norm, called at yoco/tasks/zero1_fast.py:150,157): per-workgroup FP64 partials over a fixed
+ * decomposition into `partials` (Z1_NORM_PARTIALS doubles), no atomics. */
+int z1_grad_sumsq(const z1_table* table, double* partials, void* stream);
+
+/* Fixed-order final reduction of the partials and the clip chain of yoco/tasks/zero1_fast.py:150-160 on device:
+ *   n_r = fp32(sqrt(sum)); sq = n_r*n_r; norm = sqrt(sq); grad_norm = factor*norm;
+ *   if max_norm > 0: factor *= min(fp32(1/(grad_norm + 1e-6)) * max_norm, 1)   (NaN propagates)
+ * The factor is read from factor_in (device fp32 scalar) or, when factor_in is NULL, is factor_value (a host
+ * value, e.g. fairseq's Python-float _multiply_factor).  The new factor goes to factor_out (nullable; may equal
+ * factor_in).  norm_out / grad_norm_out (device fp32 scalars) are nullable. */
+int z1_norm_clip(const double* partials, const float* factor_in, float factor_value, float* norm_out,
+                 float* grad_norm_out, float* factor_out, float max_norm, void* stream);
+
+/* The clip chain entered at `norm` (device fp32), for callers that post-process the norm (aggregate_norm_fn,
+ * yoco/tasks/zero1_fast.py:153-160): grad_norm = factor*norm; clip as above.  Factor arguments as above. */
+int z1_clip_factor(const float* norm, const float* factor_in, float factor_value, float* grad_norm_out,
+                   float* factor_out, float max_norm, void* stream);
+
+/* Fused Adam + BF16 copy over every row of the table in one persistent-grid launch (replaces the per-tensor
+ * Triton _adam launches of yoco/tasks/fused_adam_cast.py:19-45,62-72, and folds the gradient factor multiply of
+ * yoco/tasks/zero1_fast.py:175-192 / scale_up :75-89 into the gradient load).  factor: device fp32 scalar or NULL
+ * (1.0).  lr .. weight_decay are the fp32 kernel scalars; bc1, bc2 as fused_adam_cast.py:58-60 rounds them. */
+int z1_adam_cast(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
+                 float bc1, float bc2, float weight_decay, int mode, void* stream);
+
+/* g32[i] = fp32(float(g16[i]) * factor[0]) (yoco/tasks/fused_adam_cast.py:75-89). */
+int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n, void* stream);
+
+/* p16[i] = bf16(p32[i]) (the leftover casts of yoco/tasks/zero1_fast.py:198-209). */
+int z1_cast_bf16(const float* p32, uint16_t* p16, int64_t n, void* stream);
+
+/* Text for a return code (negative: argument errors; positive: hipError_t). */
+const char* z1_strerror(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YOCO_Z1_H */
