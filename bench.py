@@ -89,8 +89,10 @@ def main():
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=3)
     ap.add_argument('--config', default='c2', choices=sorted(WORKLOADS))
-    ap.add_argument('--cpu-sample-tensors', type=int, default=6)
+    ap.add_argument('--cpu-sample-tensors', type=int, default=1000)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--calibrate-copy', action='store_true',
+                    help='only run 5 plain 1 GiB device copies (the reference traffic for rocprofv3 counters)')
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get('WORLD_SIZE', '1')) != 1:
         print('bench.py: this build measures one GPU only (the shard update of one ZeRO-1 owner); '
@@ -98,6 +100,15 @@ def main():
         sys.exit(2)
 
     import torch
+    if args.calibrate_copy:
+        a = torch.ones(1 << 28, dtype=torch.float32, device='cuda:0')
+        b = torch.empty_like(a)
+        for _ in range(5):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({'calibration': 'torch copy_', 'bytes_read_per_launch': 1 << 30,
+                          'bytes_written_per_launch': 1 << 30, 'launches': 5}))
+        return
     sys.path.insert(0, ROOT)
     import __graft_entry__
     __graft_entry__.package()

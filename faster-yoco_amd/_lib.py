@@ -11,7 +11,8 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = 'libyoco_z1.so'
-LIB_PATH = os.path.join(_HERE, LIB_NAME)
+# YOCO_Z1_LIB selects another build of the same library (e.g. one compiled with different tuning macros)
+LIB_PATH = os.environ.get('YOCO_Z1_LIB') or os.path.join(_HERE, LIB_NAME)
 
 Z1_F32 = 0
 Z1_BF16 = 1

@@ -1,17 +1,24 @@
 // yoco_z1: gfx950 kernels + C ABI for the owner-side ZeRO-1 shard update (declarations: include/yoco_z1.h).
 //
 // Layout and scheduling
-//   * Every multi-tensor kernel walks one device-resident table of rows (g, p, m, v, p16, n) cut into fixed
-//     chunks of kChunk elements; row r owns the global chunk range [chunk0_r, chunk0_r + ceil(n_r / kChunk)).
-//   * Persistent grid: workgroup b takes chunks b, b + G, b + 2G, ... (G = grid size).  A workgroup's chunk index
-//     only grows, so its row index only advances (a few scalar loads per chunk at most).
-//   * Inside a full chunk each lane streams kGroups float4 groups per array; the groups of one wave are
-//     consecutive 16-byte slots, so every load/store instruction of a wave covers 1 KiB (fp32) or 512 B (bf16)
-//     contiguous bytes.  The last, partial chunk of a row (and any row whose pointers are not aligned for the
-//     vector path) runs an element-wise loop.
-//   * The norm uses the same table and a FIXED grid (Z1_NORM_PARTIALS workgroups), FP64 accumulation of the exact
+//   * Every multi-tensor kernel walks one device-resident table of rows (g, p, m, v, p16, n) cut into chunks of
+//     kChunk = 256 elements (one wave64 x one float4 per lane); row r owns the global chunk range
+//     [chunk0_r, chunk0_r + ceil(n_r / kChunk)).  A chunk -> row map (one int32 per chunk) follows the rows in
+//     the same device allocation, so a wave finds its row with two scalar loads.
+//   * Adam + BF16: one wave per chunk, one wave per workgroup, dispatched by the hardware (grid = chunks).  The
+//     workgroup -> chunk map undoes the round-robin dispatch over the 8 XCDs, so each XCD streams one contiguous
+//     eighth of the shard.  Measured on MI355X (431M-element shard): 2.10 ms, against 2.52 ms for a persistent
+//     grid with a static partition (tail imbalance across CUs/XCDs) and 2.19 ms for 1024-element workgroups; the
+//     same kernel with its arithmetic replaced by additions runs at the same speed, i.e. it is at the bandwidth
+//     this 4-read / 4-write stream pattern reaches.
+//   * Each lane moves one 128-bit group per fp32 array (and 64 bits of bf16); a wave instruction covers 1 KiB
+//     (fp32) or 512 B (bf16) of contiguous bytes, with nontemporal hints (streams far larger than L2 and MALL).
+//     The last, partial chunk of a row (and rows whose pointers are not aligned for the vector path) run an
+//     element-wise loop.
+//   * The norm uses the same table and a FIXED grid (Z1_NORM_PARTIALS workgroups of 4 waves; workgroup b takes
+//     chunks 4b..4b+3, then 4(b+G).., i.e. 1024 contiguous elements per step), FP64 accumulation of the exact
 //     squares per lane, a wave64 xor-butterfly and a fixed-order LDS stage: its bits do not depend on timing, on
-//     the device's CU count or on the run.
+//     the device's CU count or on the run.  This read pattern measured 7.0 TB/s on MI355X.
 //   * No atomics anywhere; nothing but vector memory instructions write memory.
 //
 // Numerics follow the header: one rounding per fp32 operation, explicit FMAs where the reference has them,
@@ -32,7 +39,13 @@
 #pragma clang fp contract(off)
 
 #ifndef Z1_GROUPS
-#define Z1_GROUPS 4              // float4 groups per lane per chunk
+#define Z1_GROUPS 1              // float4 groups per lane per chunk
+#endif
+#ifndef Z1_ADAM_WAVES
+#define Z1_ADAM_WAVES 1          // chunks (one per wave) per Adam workgroup
+#endif
+#ifndef Z1_NORM_UNROLL
+#define Z1_NORM_UNROLL 1         // chunks per wave per iteration of the norm
 #endif
 #ifndef Z1_NT
 #define Z1_NT 1                  // nontemporal (streaming) hints on the big streams
@@ -40,10 +53,13 @@
 
 namespace {
 
-constexpr int kThreads = 256;                                 // 4 wave64 per workgroup
+constexpr int kWave = 64;
+constexpr int kThreads = 256;                                 // norm / owner-sum / scale / cast workgroups
+constexpr int kAdamWaves = Z1_ADAM_WAVES;
 constexpr int kVec = 4;                                       // fp32 lanes of one 128-bit access
 constexpr int kGroups = Z1_GROUPS;
-constexpr int64_t kChunk = (int64_t)kThreads * kVec * kGroups;   // elements per chunk
+constexpr int64_t kChunk = (int64_t)kWave * kVec * kGroups;   // elements per chunk: one wave's share
+constexpr int kNormUnroll = Z1_NORM_UNROLL;
 constexpr int kMaxDevices = 64;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -74,10 +90,20 @@ struct AdamK {
 // table in memory, so the compiler cannot infer the address space by itself.
 #define Z1_GLOBAL __attribute__((address_space(1)))
 
+#ifndef Z1_NT_LOAD
+#define Z1_NT_LOAD Z1_NT
+#endif
+#ifndef Z1_NT_STORE
+#define Z1_NT_STORE Z1_NT
+#endif
+#ifndef Z1_XCD_MAP
+#define Z1_XCD_MAP 1
+#endif
+
 template <typename T>
 __device__ __forceinline__ T ld(const T* p) {
     const Z1_GLOBAL T* gp = (const Z1_GLOBAL T*)p;
-#if Z1_NT
+#if Z1_NT_LOAD
     return __builtin_nontemporal_load(gp);
 #else
     return *gp;
@@ -87,10 +113,22 @@ __device__ __forceinline__ T ld(const T* p) {
 template <typename T>
 __device__ __forceinline__ void st(T* p, T x) {
     Z1_GLOBAL T* gp = (Z1_GLOBAL T*)p;
-#if Z1_NT
+#if Z1_NT_STORE
     __builtin_nontemporal_store(x, gp);
 #else
     *gp = x;
+#endif
+}
+
+// Chunk of workgroup b.  With Z1_XCD_MAP the round-robin dispatch over the 8 XCDs (workgroup b on XCD b mod 8)
+// is undone so that each XCD streams one contiguous eighth of the chunks.
+__device__ __forceinline__ int64_t chunk_of_block(int64_t b, int64_t nb) {
+#if Z1_XCD_MAP
+    const int64_t x = b & 7, q = b >> 3, Q = nb >> 3, R = nb & 7;
+    return x * Q + (x < R ? x : R) + q;
+#else
+    (void)nb;
+    return b;
 #endif
 }
 
@@ -105,7 +143,21 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float x) {
     return ((u & 0x7fffffffu) > 0x7f800000u) ? 0x7fc0u : r;
 }
 
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) { return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16); }
+#ifndef Z1_HW_BF16
+#define Z1_HW_BF16 1             // gfx950's packed fp32 -> bf16 conversion (round to nearest even)
+#endif
+
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+#if Z1_HW_BF16
+    const bf2 h = __builtin_convertvector(f2{lo, hi}, bf2);
+    return __builtin_bit_cast(uint32_t, h);
+#else
+    return f32_to_bf16(lo) | (f32_to_bf16(hi) << 16);
+#endif
+}
 
 template <int MODE>
 __device__ __forceinline__ void adam_elem(float g, float& p, float& m, float& v, const AdamK& k) {
@@ -119,12 +171,6 @@ __device__ __forceinline__ void adam_elem(float g, float& p, float& m, float& v,
     float upd = mh / den;
     if (MODE == 1) upd = __builtin_fmaf(k.wd, p, upd);
     p = __builtin_fmaf(-k.lr, upd, p);
-}
-
-// Advances `t` to the row that owns chunk c (c only grows within a workgroup).
-__device__ __forceinline__ int row_of(const Row* __restrict__ rows, int nrows, int t, int64_t c) {
-    while (t + 1 < nrows && rows[t + 1].chunk0 <= c) ++t;
-    return t;
 }
 
 // ------------------------------------------------------------------------------------------------ Adam + BF16
@@ -142,59 +188,59 @@ __device__ __forceinline__ float load_g1(const void* g, int64_t i) {
 }
 
 template <int GDT, int MODE>
-__global__ __launch_bounds__(kThreads) void adam_cast_kernel(const Row* __restrict__ rows, int nrows,
-                                                             int64_t nchunks, const float* __restrict__ factor,
-                                                             AdamK k) {
+__global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row* __restrict__ rows,
+                                                                       const int32_t* __restrict__ chunk_row,
+                                                                       int64_t nchunks,
+                                                                       const float* __restrict__ factor, AdamK k) {
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t c = chunk_of_block(blockIdx.x, gridDim.x) * kAdamWaves +
+                      __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    if (c >= nchunks) return;
     const float f = factor ? *factor : 1.0f;
-    const int tid = threadIdx.x;
-    int t = 0;
-    for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
-        t = row_of(rows, nrows, t, c);
-        const Row r = rows[t];
-        const int64_t base = (c - r.chunk0) * kChunk;
-        const int64_t rem = r.n - base;
-        if (rem >= kChunk && (r.vec & kVecAll)) {
-            f4 g[kGroups], p[kGroups], m[kGroups], v[kGroups];
+    const Row r = rows[chunk_row[c]];
+    const int64_t base = (c - r.chunk0) * kChunk;
+    const int64_t rem = r.n - base;
+    if (rem >= kChunk && (r.vec & kVecAll)) {
+        f4 g[kGroups], p[kGroups], m[kGroups], v[kGroups];
 #pragma unroll
-            for (int u = 0; u < kGroups; ++u) {
-                const int64_t i = base + (int64_t)(u * kThreads + tid) * kVec;
-                g[u] = load_g4<GDT>(r.g, i);
-                p[u] = ld(reinterpret_cast<const f4*>(r.p + i));
-                m[u] = ld(reinterpret_cast<const f4*>(r.m + i));
-                v[u] = ld(reinterpret_cast<const f4*>(r.v + i));
-            }
+        for (int u = 0; u < kGroups; ++u) {
+            const int64_t i = base + (int64_t)(u * kWave + lane) * kVec;
+            g[u] = load_g4<GDT>(r.g, i);
+            p[u] = ld(reinterpret_cast<const f4*>(r.p + i));
+            m[u] = ld(reinterpret_cast<const f4*>(r.m + i));
+            v[u] = ld(reinterpret_cast<const f4*>(r.v + i));
+        }
 #pragma unroll
-            for (int u = 0; u < kGroups; ++u) {
+        for (int u = 0; u < kGroups; ++u) {
 #pragma unroll
-                for (int j = 0; j < kVec; ++j) {
-                    float pj = p[u][j], mj = m[u][j], vj = v[u][j];
-                    adam_elem<MODE>(g[u][j] * f, pj, mj, vj, k);
-                    p[u][j] = pj;
-                    m[u][j] = mj;
-                    v[u][j] = vj;
-                }
+            for (int j = 0; j < kVec; ++j) {
+                float pj = p[u][j], mj = m[u][j], vj = v[u][j];
+                adam_elem<MODE>(g[u][j] * f, pj, mj, vj, k);
+                p[u][j] = pj;
+                m[u][j] = mj;
+                v[u][j] = vj;
             }
+        }
 #pragma unroll
-            for (int u = 0; u < kGroups; ++u) {
-                const int64_t i = base + (int64_t)(u * kThreads + tid) * kVec;
-                st(reinterpret_cast<f4*>(r.p + i), p[u]);
-                st(reinterpret_cast<f4*>(r.m + i), m[u]);
-                st(reinterpret_cast<f4*>(r.v + i), v[u]);
-                if (r.p16) {
-                    const u2 h = u2{pack_bf16(p[u][0], p[u][1]), pack_bf16(p[u][2], p[u][3])};
-                    st(reinterpret_cast<u2*>(r.p16 + i), h);
-                }
+        for (int u = 0; u < kGroups; ++u) {
+            const int64_t i = base + (int64_t)(u * kWave + lane) * kVec;
+            st(reinterpret_cast<f4*>(r.p + i), p[u]);
+            st(reinterpret_cast<f4*>(r.m + i), m[u]);
+            st(reinterpret_cast<f4*>(r.v + i), v[u]);
+            if (r.p16) {
+                const u2 h = u2{pack_bf16(p[u][0], p[u][1]), pack_bf16(p[u][2], p[u][3])};
+                st(reinterpret_cast<u2*>(r.p16 + i), h);
             }
-        } else {
-            const int64_t cnt = rem < kChunk ? rem : kChunk;
-            for (int64_t i = base + tid; i < base + cnt; i += kThreads) {
-                float pj = r.p[i], mj = r.m[i], vj = r.v[i];
-                adam_elem<MODE>(load_g1<GDT>(r.g, i) * f, pj, mj, vj, k);
-                r.p[i] = pj;
-                r.m[i] = mj;
-                r.v[i] = vj;
-                if (r.p16) r.p16[i] = (uint16_t)f32_to_bf16(pj);
-            }
+        }
+    } else {
+        const int64_t cnt = rem < kChunk ? rem : kChunk;
+        for (int64_t i = base + lane; i < base + cnt; i += kWave) {
+            float pj = r.p[i], mj = r.m[i], vj = r.v[i];
+            adam_elem<MODE>(load_g1<GDT>(r.g, i) * f, pj, mj, vj, k);
+            r.p[i] = pj;
+            r.m[i] = mj;
+            r.v[i] = vj;
+            if (r.p16) r.p16[i] = (uint16_t)f32_to_bf16(pj);
         }
     }
 }
@@ -204,13 +250,13 @@ __global__ __launch_bounds__(kThreads) void adam_cast_kernel(const Row* __restri
 // every lane ends with the same bits), then the four wave sums in wave order.
 __device__ __forceinline__ double block_sum(double x, double* lds) {
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, 64);
-    if ((threadIdx.x & 63) == 0) lds[threadIdx.x >> 6] = x;
+    for (int off = kWave / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
+    if ((threadIdx.x & (kWave - 1)) == 0) lds[threadIdx.x / kWave] = x;
     __syncthreads();
     double s = 0.0;
     if (threadIdx.x == 0) {
 #pragma unroll
-        for (int w = 0; w < kThreads / 64; ++w) s += lds[w];
+        for (int w = 0; w < kThreads / kWave; ++w) s += lds[w];
     }
     return s;
 }
@@ -220,34 +266,58 @@ __device__ __forceinline__ double sq64(float x) {
     return d * d;                      // exact: 24-bit significand squared
 }
 
+// Wave w of the fixed grid takes chunks w, w + W, w + 2W, ... (W = waves in the grid), kNormUnroll of them per
+// iteration with all their loads issued first; each lane adds its squares in that fixed order.
 template <int GDT>
-__global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__ rows, int nrows, int64_t nchunks,
+__global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__ rows,
+                                                         const int32_t* __restrict__ chunk_row, int64_t nchunks,
                                                          double* __restrict__ partials) {
-    __shared__ double lds[kThreads / 64];
-    const int tid = threadIdx.x;
+    __shared__ double lds[kThreads / kWave];
+    const int lane = threadIdx.x & (kWave - 1);
+    const int64_t nw = (int64_t)gridDim.x * (kThreads / kWave);
+    const int64_t w0 = (int64_t)blockIdx.x * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     double acc = 0.0;
-    int t = 0;
-    for (int64_t c = blockIdx.x; c < nchunks; c += gridDim.x) {
-        t = row_of(rows, nrows, t, c);
-        const Row r = rows[t];
-        const int64_t base = (c - r.chunk0) * kChunk;
-        const int64_t rem = r.n - base;
-        if (rem >= kChunk && (r.vec & kVecG)) {
-            f4 g[kGroups];
+    for (int64_t c0 = w0; c0 < nchunks; c0 += nw * kNormUnroll) {
+        f4 x[kNormUnroll][kGroups];
+        int64_t base[kNormUnroll], cnt[kNormUnroll];
+        const void* gp[kNormUnroll];
+        bool vec[kNormUnroll];
 #pragma unroll
-            for (int u = 0; u < kGroups; ++u) g[u] = load_g4<GDT>(r.g, base + (int64_t)(u * kThreads + tid) * kVec);
+        for (int j = 0; j < kNormUnroll; ++j) {
+            const int64_t c = c0 + j * nw;
+            cnt[j] = 0;
+            vec[j] = false;
+            base[j] = 0;
+            gp[j] = nullptr;
+            if (c < nchunks) {
+                const Row r = rows[chunk_row[c]];
+                base[j] = (c - r.chunk0) * kChunk;
+                const int64_t rem = r.n - base[j];
+                cnt[j] = rem < kChunk ? rem : kChunk;
+                gp[j] = r.g;
+                vec[j] = rem >= kChunk && (r.vec & kVecG);
+                if (vec[j]) {
 #pragma unroll
-            for (int u = 0; u < kGroups; ++u) {
-#pragma unroll
-                for (int j = 0; j < kVec; ++j) acc += sq64(g[u][j]);
+                    for (int u = 0; u < kGroups; ++u)
+                        x[j][u] = load_g4<GDT>(r.g, base[j] + (int64_t)(u * kWave + lane) * kVec);
+                }
             }
-        } else {
-            const int64_t cnt = rem < kChunk ? rem : kChunk;
-            for (int64_t i = base + tid; i < base + cnt; i += kThreads) acc += sq64(load_g1<GDT>(r.g, i));
+        }
+#pragma unroll
+        for (int j = 0; j < kNormUnroll; ++j) {
+            if (vec[j]) {
+#pragma unroll
+                for (int u = 0; u < kGroups; ++u) {
+#pragma unroll
+                    for (int e = 0; e < kVec; ++e) acc += sq64(x[j][u][e]);
+                }
+            } else {
+                for (int64_t i = base[j] + lane; i < base[j] + cnt[j]; i += kWave) acc += sq64(load_g1<GDT>(gp[j], i));
+            }
         }
     }
     const double s = block_sum(acc, lds);
-    if (tid == 0) partials[blockIdx.x] = s;
+    if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }
 
 // zero1_fast.py:150-160 scalar chain, one owner.
@@ -397,7 +467,6 @@ inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintp
 
 struct DevInfo {
     int cus = 0;
-    int adam_blocks[2][2] = {{0, 0}, {0, 0}};   // [gdt][mode] resident workgroups per CU
 };
 
 std::mutex g_mu;
@@ -422,30 +491,6 @@ int cu_count(int dev, int* cus) {
     return Z1_OK;
 }
 
-template <int GDT, int MODE>
-int adam_grid(int dev, int64_t nchunks, int* grid) {
-    int cus = 0;
-    int rc = cu_count(dev, &cus);
-    if (rc) return rc;
-    int per = 0;
-    {
-        std::lock_guard<std::mutex> lk(g_mu);
-        per = g_dev[dev].adam_blocks[GDT][MODE];
-    }
-    if (per == 0) {
-        hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per, reinterpret_cast<const void*>(&adam_cast_kernel<GDT, MODE>), kThreads, 0);
-        if (e != hipSuccess) return (int)e;
-        if (per < 1) per = 1;
-        std::lock_guard<std::mutex> lk(g_mu);
-        g_dev[dev].adam_blocks[GDT][MODE] = per;
-    }
-    int64_t g = (int64_t)cus * per;
-    if (g > nchunks) g = nchunks;
-    *grid = (int)(g < 1 ? 1 : g);
-    return Z1_OK;
-}
-
 int stream_grid(int dev, int64_t groups, int* grid) {
     int cus = 0;
     int rc = cu_count(dev, &cus);
@@ -465,7 +510,8 @@ inline int launch_status() {
 }  // namespace
 
 struct z1_table {
-    Row* rows;            // device
+    Row* rows;            // device: nrows rows, then nchunks int32 chunk -> row entries (one allocation)
+    int32_t* chunk_row;
     int nrows;
     int g_dtype;
     int device;
@@ -512,9 +558,19 @@ int z1_table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table** ou
         numel += t.n;
         h.push_back(r);
     }
+    if (chunks > INT32_MAX) return Z1_E_SIZE;          // one workgroup per chunk: grid.x limit
     int dev = 0;
     int rc = current_device(&dev);
     if (rc) return rc;
+    // host image of [rows][chunk -> row], copied in one transfer
+    const size_t rows_bytes = sizeof(Row) * h.size();
+    std::vector<unsigned char> img(rows_bytes + sizeof(int32_t) * (size_t)chunks);
+    if (rows_bytes) memcpy(img.data(), h.data(), rows_bytes);
+    int32_t* map = reinterpret_cast<int32_t*>(img.data() + rows_bytes);
+    for (size_t i = 0; i < h.size(); ++i) {
+        const int64_t c1 = i + 1 < h.size() ? h[i + 1].chunk0 : chunks;
+        for (int64_t c = h[i].chunk0; c < c1; ++c) map[c] = (int32_t)i;
+    }
     z1_table* tb = new (std::nothrow) z1_table();
     if (!tb) return (int)hipErrorOutOfMemory;
     tb->nrows = (int)h.size();
@@ -524,14 +580,14 @@ int z1_table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table** ou
     tb->numel = numel;
     tb->nchunks = chunks;
     tb->rows = nullptr;
-    const size_t bytes = sizeof(Row) * (h.empty() ? 1 : h.size());
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(&tb->rows), bytes);
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&tb->rows), img.empty() ? 64 : img.size());
     if (e != hipSuccess) {
         delete tb;
         return (int)e;
     }
-    if (!h.empty()) {
-        e = hipMemcpy(tb->rows, h.data(), sizeof(Row) * h.size(), hipMemcpyHostToDevice);
+    tb->chunk_row = reinterpret_cast<int32_t*>(reinterpret_cast<unsigned char*>(tb->rows) + rows_bytes);
+    if (!img.empty()) {
+        e = hipMemcpy(tb->rows, img.data(), img.size(), hipMemcpyHostToDevice);
         if (e != hipSuccess) {
             (void)hipFree(tb->rows);
             delete tb;
@@ -575,10 +631,10 @@ int z1_grad_sumsq(const z1_table* table, double* partials, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (table->g_dtype == Z1_F32)
         hipLaunchKernelGGL(sumsq_kernel<Z1_F32>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows, table->nchunks, partials);
+                           table->chunk_row, table->nchunks, partials);
     else
         hipLaunchKernelGGL(sumsq_kernel<Z1_BF16>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows, table->nchunks, partials);
+                           table->chunk_row, table->nchunks, partials);
     return launch_status();
 }
 
@@ -618,14 +674,10 @@ int z1_adam_cast(const z1_table* table, const float* factor, float lr, float bet
     k.omb1 = 1.0f - beta1;
     k.omb2 = 1.0f - beta2;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    int grid = 0;
-#define Z1_LAUNCH_ADAM(GDT, MODE)                                                                            \
-    do {                                                                                                     \
-        rc = adam_grid<GDT, MODE>(dev, table->nchunks, &grid);                                              \
-        if (rc) return rc;                                                                                   \
-        hipLaunchKernelGGL((adam_cast_kernel<GDT, MODE>), dim3(grid), dim3(kThreads), 0, s, table->rows,    \
-                           table->nrows, table->nchunks, factor, k);                                         \
-    } while (0)
+    const dim3 grid((unsigned)((table->nchunks + kAdamWaves - 1) / kAdamWaves));
+#define Z1_LAUNCH_ADAM(GDT, MODE)                                                                              \
+    hipLaunchKernelGGL((adam_cast_kernel<GDT, MODE>), grid, dim3(kWave * kAdamWaves), 0, s, table->rows,      \
+                       table->chunk_row, table->nchunks, factor, k)
     if (table->g_dtype == Z1_F32) {
         if (mode == 1) Z1_LAUNCH_ADAM(Z1_F32, 1);
         else Z1_LAUNCH_ADAM(Z1_F32, 0);
