@@ -44,9 +44,6 @@
 #ifndef Z1_ADAM_WAVES
 #define Z1_ADAM_WAVES 1          // chunks (one per wave) per Adam workgroup
 #endif
-#ifndef Z1_NORM_UNROLL
-#define Z1_NORM_UNROLL 1         // chunks per wave per iteration of the norm
-#endif
 #ifndef Z1_NT
 #define Z1_NT 1                  // nontemporal (streaming) hints on the big streams
 #endif
@@ -59,7 +56,6 @@ constexpr int kAdamWaves = Z1_ADAM_WAVES;
 constexpr int kVec = 4;                                       // fp32 lanes of one 128-bit access
 constexpr int kGroups = Z1_GROUPS;
 constexpr int64_t kChunk = (int64_t)kWave * kVec * kGroups;   // elements per chunk: one wave's share
-constexpr int kNormUnroll = Z1_NORM_UNROLL;
 constexpr int kMaxDevices = 64;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -266,54 +262,47 @@ __device__ __forceinline__ double sq64(float x) {
     return d * d;                      // exact: 24-bit significand squared
 }
 
-// Wave w of the fixed grid takes chunks w, w + W, w + 2W, ... (W = waves in the grid), kNormUnroll of them per
-// iteration with all their loads issued first; each lane adds its squares in that fixed order.
+// Last row whose first chunk is <= c, searching forward from row t (c only grows within a wave).  The rows table
+// is a few KiB and stays in the scalar cache; the chunk -> row map is not read here (it would add ~3% traffic).
+__device__ __forceinline__ int advance_row(const Row* __restrict__ rows, int nrows, int t, int64_t c) {
+    if (t + 1 >= nrows || rows[t + 1].chunk0 > c) return t;
+    int lo = t + 1, hi = nrows - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (rows[mid].chunk0 <= c) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Wave w of the fixed grid takes chunks w, w + W, w + 2W, ... (W = waves in the grid: a workgroup covers 4
+// consecutive chunks = 1024 contiguous elements per step); each lane adds its exact squares in that fixed order.
 template <int GDT>
-__global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__ rows,
-                                                         const int32_t* __restrict__ chunk_row, int64_t nchunks,
+__global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__ rows, int nrows, int64_t nchunks,
                                                          double* __restrict__ partials) {
     __shared__ double lds[kThreads / kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t nw = (int64_t)gridDim.x * (kThreads / kWave);
     const int64_t w0 = (int64_t)blockIdx.x * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
     double acc = 0.0;
-    for (int64_t c0 = w0; c0 < nchunks; c0 += nw * kNormUnroll) {
-        f4 x[kNormUnroll][kGroups];
-        int64_t base[kNormUnroll], cnt[kNormUnroll];
-        const void* gp[kNormUnroll];
-        bool vec[kNormUnroll];
+    int t = 0;
+    for (int64_t c = w0; c < nchunks; c += nw) {
+        t = advance_row(rows, nrows, t, c);
+        const Row r = rows[t];
+        const int64_t base = (c - r.chunk0) * kChunk;
+        const int64_t rem = r.n - base;
+        if (rem >= kChunk && (r.vec & kVecG)) {
+            f4 x[kGroups];
 #pragma unroll
-        for (int j = 0; j < kNormUnroll; ++j) {
-            const int64_t c = c0 + j * nw;
-            cnt[j] = 0;
-            vec[j] = false;
-            base[j] = 0;
-            gp[j] = nullptr;
-            if (c < nchunks) {
-                const Row r = rows[chunk_row[c]];
-                base[j] = (c - r.chunk0) * kChunk;
-                const int64_t rem = r.n - base[j];
-                cnt[j] = rem < kChunk ? rem : kChunk;
-                gp[j] = r.g;
-                vec[j] = rem >= kChunk && (r.vec & kVecG);
-                if (vec[j]) {
+            for (int u = 0; u < kGroups; ++u) x[u] = load_g4<GDT>(r.g, base + (int64_t)(u * kWave + lane) * kVec);
 #pragma unroll
-                    for (int u = 0; u < kGroups; ++u)
-                        x[j][u] = load_g4<GDT>(r.g, base[j] + (int64_t)(u * kWave + lane) * kVec);
-                }
+            for (int u = 0; u < kGroups; ++u) {
+#pragma unroll
+                for (int e = 0; e < kVec; ++e) acc += sq64(x[u][e]);
             }
-        }
-#pragma unroll
-        for (int j = 0; j < kNormUnroll; ++j) {
-            if (vec[j]) {
-#pragma unroll
-                for (int u = 0; u < kGroups; ++u) {
-#pragma unroll
-                    for (int e = 0; e < kVec; ++e) acc += sq64(x[j][u][e]);
-                }
-            } else {
-                for (int64_t i = base[j] + lane; i < base[j] + cnt[j]; i += kWave) acc += sq64(load_g1<GDT>(gp[j], i));
-            }
+        } else {
+            const int64_t cnt = rem < kChunk ? rem : kChunk;
+            for (int64_t i = base + lane; i < base + cnt; i += kWave) acc += sq64(load_g1<GDT>(r.g, i));
         }
     }
     const double s = block_sum(acc, lds);
@@ -631,10 +620,10 @@ int z1_grad_sumsq(const z1_table* table, double* partials, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     if (table->g_dtype == Z1_F32)
         hipLaunchKernelGGL(sumsq_kernel<Z1_F32>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->chunk_row, table->nchunks, partials);
+                           table->nrows, table->nchunks, partials);
     else
         hipLaunchKernelGGL(sumsq_kernel<Z1_BF16>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->chunk_row, table->nchunks, partials);
+                           table->nrows, table->nchunks, partials);
     return launch_status();
 }
 

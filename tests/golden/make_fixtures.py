@@ -1,0 +1,79 @@
+"""Writes the committed golden fixtures (inputs + oracle outputs) for the parity suite.
+
+    python tests/golden/make_fixtures.py
+
+Each fixture is an .npz (no pickles) holding the inputs of a small update and the CPU oracle's outputs:
+owner-sum average (c3), the norm n_r, grad_norm, the clipped factor, and the Adam outputs p, m, v, p16 computed
+with that factor.  They are produced by this build's oracle (oracle/z1_oracle.c), not by the reference: the
+reference ships no vectors for this path.
+"""
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+import oracle  # noqa: E402
+
+HP = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+MAX_NORM = 1.0
+
+MINI = [(32, 32), (128, 32), (32, 128), (32,), (33, 7)]
+
+
+def _inputs(n, seed, kind, step1):
+    rng = np.random.default_rng(seed)
+    p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+    m = np.zeros(n, np.float32) if step1 else (rng.standard_normal(n) * 1e-4).astype(np.float32)
+    v = np.zeros(n, np.float32) if step1 else np.abs(rng.standard_normal(n) * 1e-8).astype(np.float32)
+    if kind == 'student_t':
+        u = (rng.integers(0, 1 << 24, n).astype(np.float64) + 0.5) / float(1 << 24)
+        g = (2.0 * u - 1.0) / np.sqrt(2.0 * u * (1.0 - u)) * 1e-3
+        k = max(1, int(round(1e-3 * n)))
+        idx = rng.choice(n, size=k, replace=False)
+        g[idx] = np.where(rng.integers(0, 2, k) == 1, 1e4, -1e4)
+        g = g.astype(np.float32)
+    else:
+        g = (rng.standard_normal(n) * (1e-3 if step1 else 1e-4)).astype(np.float32)
+    return g, p, m, v
+
+
+def make(name, shapes, seed, kind='normal', step=1, owner=False):
+    sizes = [int(np.prod(s)) for s in shapes]
+    n = sum(sizes)
+    g, p, m, v = _inputs(n, seed, kind, step == 1)
+    out = {'shapes': np.array([list(s) + [0] * (2 - len(s)) for s in shapes], np.int64),
+           'sizes': np.array(sizes, np.int64), 'step': np.int64(step), 'p': p, 'm': m, 'v': v,
+           'hp': np.array([HP['lr'], HP['beta1'], HP['beta2'], HP['eps'], HP['weight_decay'], MAX_NORM])}
+    if owner:
+        rng = np.random.default_rng(seed + 100)
+        contribs = np.stack([oracle.bf16_rne((rng.standard_normal(n) * 1e-3).astype(np.float32))
+                             for _ in range(8)])
+        avg16, s = oracle.owner_sum(list(contribs), want_sum=True)
+        out.update(contribs=contribs, avg16=avg16, sum32=s)
+        gin = avg16
+    else:
+        out['g'] = g
+        gin = g
+    ss = oracle.sumsq(gin)
+    nr, gn, fac = oracle.norm_clip(ss, 1.0, MAX_NORM)
+    po, mo, vo, p16 = oracle.adam_cast(gin, p, m, v, step=step, factor=fac, **HP)
+    out.update(norm=np.float32(nr), grad_norm=np.float32(gn), factor=np.float32(fac), p_out=po, m_out=mo, v_out=vo,
+               p16_out=p16)
+    np.savez_compressed(os.path.join(HERE, f'{name}.npz'), **out)
+    return out
+
+
+def main():
+    make('c1_mini', MINI, seed=1, step=1)
+    make('c2_mini', MINI, seed=2, step=1000)
+    make('c3_mini', [(2048,), (3, 333), (64,)], seed=3, step=1000, owner=True)
+    make('c5_mini', MINI, seed=5, kind='student_t', step=1000)
+    print('fixtures written to', HERE)
+
+
+if __name__ == '__main__':
+    main()

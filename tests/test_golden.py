@@ -1,0 +1,96 @@
+"""Committed golden fixtures (tests/golden/*.npz, written by tests/golden/make_fixtures.py from the CPU oracle).
+
+CPU: the oracle still reproduces every fixture bit for bit (a regression pin on the oracle itself).
+GPU: the HIP path reproduces them -- owner sum, Adam m / v / master and the BF16 copy bit-exact given the
+fixture's clip factor, the norm within 1 fp32 ulp of the fixture's, the clip chain bit-exact given the GPU norm.
+"""
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), 'golden')
+FIXTURES = sorted(glob.glob(os.path.join(HERE, '*.npz')))
+
+
+def load(path):
+    with np.load(path, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def hp(f):
+    lr, b1, b2, eps, wd, mn = (float(x) for x in f['hp'])
+    return dict(lr=lr, beta1=b1, beta2=b2, eps=eps, weight_decay=wd), mn
+
+
+def test_fixtures_present():
+    names = {os.path.basename(p) for p in FIXTURES}
+    assert {'c1_mini.npz', 'c2_mini.npz', 'c3_mini.npz', 'c5_mini.npz'} <= names
+
+
+@pytest.mark.parametrize('path', FIXTURES, ids=[os.path.basename(p) for p in FIXTURES])
+def test_oracle_reproduces_fixture(path):
+    f = load(path)
+    h, mn = hp(f)
+    if 'contribs' in f:
+        avg, s = oracle.owner_sum(list(f['contribs']), want_sum=True)
+        assert np.array_equal(avg, f['avg16']) and np.array_equal(s.view(np.uint32), f['sum32'].view(np.uint32))
+        g = avg
+    else:
+        g = f['g']
+    nr, gn, fac = oracle.norm_clip(oracle.sumsq(g), 1.0, mn)
+    assert (nr, gn, fac) == (f['norm'], f['grad_norm'], f['factor'])
+    po, mo, vo, p16 = oracle.adam_cast(g, f['p'], f['m'], f['v'], step=int(f['step']), factor=float(f['factor']), **h)
+    for a, b in ((po, f['p_out']), (mo, f['m_out']), (vo, f['v_out'])):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.array_equal(p16, f['p16_out'])
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize('path', FIXTURES, ids=[os.path.basename(p) for p in FIXTURES])
+def test_gpu_reproduces_fixture(pkg, dev, path):
+    from faster_yoco_amd import configs, ops
+    f = load(path)
+    h, mn = hp(f)
+    sizes = [int(x) for x in f['sizes']]
+    n = sum(sizes)
+    part = ops.norm_workspace(dev)
+    if 'contribs' in f:
+        cs = [configs.to_device_bf16(c, dev) for c in f['contribs']]
+        g = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        ops.owner_sum(cs, g, 1.0 / 8, partials=part)
+        torch.cuda.synchronize()
+        assert np.array_equal(configs.bf16_bits(g), f['avg16'])
+    else:
+        g = torch.from_numpy(f['g']).to(dev)
+    p = torch.from_numpy(f['p']).to(dev)
+    m = torch.from_numpy(f['m']).to(dev)
+    v = torch.from_numpy(f['v']).to(dev)
+    p16 = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    rows, off = [], 0
+    for s in sizes:
+        sl = slice(off, off + s)
+        rows.append((g[sl], p[sl], m[sl], v[sl], p16[sl], s))
+        off += s
+    table = ops.Table(rows, dev)
+    if 'contribs' not in f:
+        ops.grad_sumsq(table, part)
+    nr = torch.zeros(1, device=dev)
+    gn = torch.zeros(1, device=dev)
+    fo = torch.zeros(1, device=dev)
+    ops.norm_clip(part, factor=1.0, norm_out=nr, grad_norm_out=gn, factor_out=fo, max_norm=mn)
+    torch.cuda.synchronize()
+    assert oracle.ulp_diff_f32(np.float32(nr.item()), f['norm']) <= 1
+    _, gn_ref, fo_ref = oracle.norm_clip(float(nr.item()) ** 2, 1.0, mn)
+    assert np.float32(gn.item()) == gn_ref and np.float32(fo.item()) == fo_ref
+    fac = torch.tensor([float(f['factor'])], dtype=torch.float32, device=dev)
+    bc1, bc2 = ops.bias_corrections(h['beta1'], h['beta2'], int(f['step']))
+    ops.adam_cast(table, fac, h['lr'], h['beta1'], h['beta2'], h['eps'], bc1, bc2, h['weight_decay'], 1)
+    torch.cuda.synchronize()
+    for t, ref in ((p, f['p_out']), (m, f['m_out']), (v, f['v_out'])):
+        assert np.array_equal(t.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    assert np.array_equal(configs.bf16_bits(p16), f['p16_out'])

@@ -1,0 +1,201 @@
+"""The reference's surfaces driven as its trainer drives them, on the GPU, checked against the oracle:
+FusedAdamCast through FusedAdamV2.step's multi_tensor_adam call, zero1_fast's clip_grad_norm / step / zero_grad
+installed on fairseq's mixin (switch combinations), and CEReduce._sum."""
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+import fakes  # noqa: E402
+
+pytestmark = pytest.mark.gpu
+
+HP = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+SHAPES = [(96, 64), (256, 33), (3072,), (7,), (64, 256)]
+
+
+def bits(t):
+    a = t.detach().cpu()
+    return a.view(torch.int16).numpy().view(np.uint16) if a.dtype == torch.bfloat16 else a.numpy().view(np.uint32)
+
+
+def bf16_params(dev, seed):
+    g = torch.Generator(device='cpu').manual_seed(seed)
+    return [torch.nn.Parameter((torch.randn(s, generator=g) * 0.02).to(torch.bfloat16).to(dev)) for s in SHAPES]
+
+
+def set_grads(params, seed, scale=1e-2):
+    g = torch.Generator(device='cpu').manual_seed(seed)
+    for p in params:
+        p.grad = (torch.randn(p.shape, generator=g) * scale).to(torch.bfloat16).to(p.device)
+
+
+# ----------------------------------------------------------------------------------------- FusedAdamCast
+def test_fused_adam_cast_through_fused_adam_v2(pkg, dev):
+    from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+    rng = np.random.default_rng(0)
+    p32 = [torch.nn.Parameter(torch.from_numpy((rng.standard_normal(s) * 0.02).astype(np.float32)).to(dev))
+           for s in SHAPES]
+    flat16 = torch.zeros(sum(p.numel() for p in p32), dtype=torch.bfloat16, device=dev)
+    views, off = [], 0
+    for p in p32:
+        views.append(flat16[off:off + p.numel()].view_as(p))
+        off += p.numel()
+    dest = {p.data_ptr(): v for p, v in zip(p32[:-1], views[:-1])}        # the last master has no bf16 copy
+    opt = fakes.FakeFusedAdamV2(p32, lr=HP['lr'], betas=(HP['beta1'], HP['beta2']), eps=HP['eps'],
+                                weight_decay=HP['weight_decay'])
+    fa = opt.multi_tensor_adam = FusedAdamCast(dest)
+    state = [(p.detach().cpu().numpy().ravel().copy(), np.zeros(p.numel(), np.float32),
+              np.zeros(p.numel(), np.float32)) for p in p32]
+    for step in (1, 2, 3):
+        gs = [(rng.standard_normal(p.numel()) * 1e-3).astype(np.float32) for p in p32]
+        for p, g in zip(p32, gs):
+            p.grad = torch.from_numpy(g.reshape(p.shape)).to(dev)
+        opt.step()
+        torch.cuda.synchronize()
+        assert fa.cast == {p.data_ptr() for p in p32[:-1]}
+        fa.cast.clear()
+        for i, (p, g) in enumerate(zip(p32, gs)):
+            po, mo, vo, p16 = oracle.adam_cast(g, *state[i], step=step, **HP)
+            st = opt.state[p]
+            assert np.array_equal(bits(p).ravel(), po.view(np.uint32))
+            assert np.array_equal(bits(st['exp_avg']).ravel(), mo.view(np.uint32))
+            assert np.array_equal(bits(st['exp_avg_sq']).ravel(), vo.view(np.uint32))
+            if i < len(p32) - 1:
+                assert np.array_equal(bits(views[i]).ravel(), p16)
+            state[i] = (po, mo, vo)
+    assert not bits(views[-1]).any()                                         # untouched
+
+
+def test_fused_adam_cast_errors(pkg, dev):
+    from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+    fa = FusedAdamCast({})
+    x = torch.zeros(8, 8, device=dev)
+    with pytest.raises(RuntimeError, match='expected contiguous fp32 tensors'):
+        fa(0, None, [[x.t()], [x], [x], [x]], 1e-3, 0.9, 0.95, 1e-8, 1, 1, 1, 0.0)
+    with pytest.raises(RuntimeError, match='expected contiguous fp32 tensors'):
+        fa(0, None, [[x.half()], [x], [x], [x]], 1e-3, 0.9, 0.95, 1e-8, 1, 1, 1, 0.0)
+    fa = FusedAdamCast({x.data_ptr(): torch.zeros(64, device=dev)})
+    with pytest.raises(RuntimeError, match='bf16 destination'):
+        fa(0, None, [[x], [x], [x.clone()], [x.clone()]], 1e-3, 0.9, 0.95, 1e-8, 1, 1, 1, 0.0)
+
+
+# ---------------------------------------------------------------------------------------------- zero1_fast
+def expected_update(params, grads16, state, step, factor0, max_norm, reduce_owner):
+    """Oracle: norm over all bf16 grads and the clip chain of zero1_fast.py:150-160 (REDUCE_OWNER: via sq and
+    sqrt) or :157-160 (grad_norm = factor * norm).  Returns (grad_norm, factor, n_r, None)."""
+    ss = sum(oracle.sumsq(g) for g in grads16)
+    nr = np.float32(np.sqrt(ss))
+    if reduce_owner:
+        _, gn, fac = oracle.norm_clip(float(nr) ** 2, factor0, max_norm)
+    else:
+        gn, fac = oracle.clip_factor(nr, factor0, max_norm)
+    return gn, fac, nr, None
+
+
+@pytest.mark.parametrize('switches', [
+    dict(ONE_PASS=True, SCALE_KERNEL=True, FOLD_SCALE=True),
+    dict(ONE_PASS=True, SCALE_KERNEL=True, FOLD_SCALE=False),
+    dict(ONE_PASS=False, SCALE_KERNEL=False, FOLD_SCALE=False),
+    dict(ONE_PASS=True, SCALE_KERNEL=True, FOLD_SCALE=True, ALLGATHER=True),
+], ids=['fold', 'scale_kernel', 'foreach', 'allgather_buffer'])
+@pytest.mark.parametrize('reduce_owner', [False, True], ids=['all_grads', 'reduce_owner'])
+def test_zero1_fast_trainer_sequence(pkg, dev, switches, reduce_owner):
+    from faster_yoco_amd import zero1_fast
+    sw = dict(ENABLED=True, FUSED_ADAM=True, ALLGATHER=False, PARAM_VIEWS=False, REDUCE_OWNER=reduce_owner)
+    sw.update(switches)
+    zero1_fast.configure(**sw)
+
+    class Mixin(fakes.FakeMixin):
+        pass
+
+    zero1_fast._ORIG.clear()
+    assert zero1_fast.install(Mixin)
+
+    class Opt(Mixin, fakes.FakeFP16Optimizer):
+        pass
+
+    params = bf16_params(dev, 1)
+    opt = Opt(params, lr=HP['lr'], betas=(HP['beta1'], HP['beta2']), eps=HP['eps'], weight_decay=HP['weight_decay'])
+    state = [(p.detach().float().cpu().numpy().ravel().copy(), np.zeros(p.numel(), np.float32),
+              np.zeros(p.numel(), np.float32)) for p in params]
+    oss = opt.fp32_optimizer.optimizer
+    for step, max_norm in ((1, 1.0), (2, 0.05), (3, 0.0)):
+        set_grads(params, 10 + step)
+        grads16 = [bits(p.grad).ravel().copy() for p in params]
+        # trainer_nosync.py:273-282: multiply_grads(numer / denom) with a device denom, then clip_grad_norm
+        denom = torch.tensor(16384.0, device=dev)
+        opt.multiply_grads(8 / denom)
+        factor0 = np.float32(opt._multiply_factor.item())
+        gn = opt.clip_grad_norm(max_norm)
+        ftensor = opt._multiply_factor                 # the clipped factor (written in place on device)
+        fac_gpu = float(ftensor.item())
+        exp_gn, exp_fac, nr, _ = expected_update(params, grads16, state, step, factor0, max_norm, reduce_owner)
+        assert gn.dim() == 0 and gn.dtype == torch.float32 and gn.is_cuda
+        got_gn = np.float32(gn.item())
+        assert abs(float(got_gn) - float(exp_gn)) <= 1e-6 * float(exp_gn) + 1e-30
+        if got_gn == exp_gn:                           # same norm bits -> the chain is bit-exact
+            assert np.float32(fac_gpu) == exp_fac
+        opt.step()
+        torch.cuda.synchronize()
+        assert opt._multiply_factor == 1.0
+        new = [oracle.adam_cast(g, *st_, step=step, factor=fac_gpu, **HP) for g, st_ in zip(grads16, state)]
+        for i, p in enumerate(params):
+            po, mo, vo, p16 = new[i]
+            st = oss.optim.state[opt.fp32_params[i]]
+            assert np.array_equal(bits(opt.fp32_params[i]).ravel(), po.view(np.uint32)), i
+            assert np.array_equal(bits(st['exp_avg']).ravel(), mo.view(np.uint32)), i
+            assert np.array_equal(bits(st['exp_avg_sq']).ravel(), vo.view(np.uint32)), i
+            assert np.array_equal(bits(p).ravel(), p16), i
+        state = [(po, mo, vo) for po, mo, vo, _ in new]
+        opt.zero_grad()
+        assert all(p.grad is None for p in params)
+    zero1_fast.configure(ENABLED=False)
+
+
+def test_zero1_fast_disabled_falls_back(pkg, dev):
+    from faster_yoco_amd import zero1_fast
+    zero1_fast.configure(ENABLED=False)
+
+    class Mixin(fakes.FakeMixin):
+        pass
+
+    assert not zero1_fast.install(Mixin)
+    zero1_fast.configure(ENABLED=True)
+    zero1_fast._ORIG.clear()
+    zero1_fast.install(Mixin)
+
+    class Opt(Mixin, fakes.FakeFP16Optimizer):
+        pass
+
+    opt = Opt(bf16_params(dev, 2))
+    opt.fp32_optimizer.optimizer = object()          # not an OSS: the reference falls back to upstream
+    with pytest.raises(AssertionError, match='upstream clip_grad_norm reached'):
+        opt.clip_grad_norm(1.0)
+    zero1_fast.configure(ENABLED=False)
+
+
+# ------------------------------------------------------------------------------------------------ CEReduce
+def test_ce_reduce_sum_installed(pkg, dev):
+    from faster_yoco_amd import ce_reduce
+    rng = np.random.default_rng(5)
+    W, G = 8, 5000
+    cls = type('CEReduce', (fakes.FakeCEReduce,), {})
+    ce_reduce.install(cls)
+    for R in (0, 6):
+        S = oracle.bf16_rne((rng.standard_normal((W - 1) * G) * 1e-3).astype(np.float32))
+        OUT = oracle.bf16_rne((rng.standard_normal(G) * 1e-3).astype(np.float32))
+        bounds = [[0, 1234], [1234, 1234], [1234, G]]
+        ce = cls(torch.from_numpy(S.view(np.int16)).to(dev).view(torch.bfloat16),
+                 torch.from_numpy(OUT.view(np.int16)).to(dev).view(torch.bfloat16), G, bounds, R, W)
+        exp = OUT.copy()
+        for ph, (a, b) in enumerate(bounds):
+            ce._sum(ph)
+            oracle.sum_slots(S, exp, G, a, b, R, 1.0 / W, W)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(ce.out), exp)
