@@ -98,9 +98,11 @@ class TableCache:
         self._d.clear()
 
 
-def norm_workspace(device):
-    """Workspace of the norm partials (Z1_NORM_PARTIALS doubles)."""
-    return torch.empty(Z1_NORM_PARTIALS, dtype=torch.float64, device=device)
+def norm_workspace(device, n=0):
+    """Workspace of the norm partials: Z1_NORM_PARTIALS doubles, or enough for a fused owner sum over n
+    elements (its first Z1_NORM_PARTIALS doubles are what norm_clip reads)."""
+    size = Z1_NORM_PARTIALS if n <= 0 else int(lib().z1_owner_sum_workspace(int(n)))
+    return torch.empty(size, dtype=torch.float64, device=device)
 
 
 def grad_sumsq(table, partials):
@@ -187,8 +189,12 @@ def owner_sum(contribs, out, scale, out_sum=None, partials=None):
         require_gpu(out_sum, 'owner_sum')
         if out_sum.dtype != torch.float32 or not out_sum.is_contiguous() or out_sum.numel() != out.numel():
             raise RuntimeError('yoco_z1: owner_sum out_sum must be a contiguous fp32 tensor like out')
-    if partials is not None and (partials.dtype != torch.float64 or partials.numel() < Z1_NORM_PARTIALS):
-        raise RuntimeError('yoco_z1: norm workspace must hold Z1_NORM_PARTIALS float64')
+    if partials is not None:
+        require_gpu(partials, 'owner_sum')
+        need = int(lib().z1_owner_sum_workspace(out.numel()))
+        if partials.dtype != torch.float64 or partials.numel() < need:
+            raise RuntimeError(f'yoco_z1: the fused-norm workspace must hold {need} float64 '
+                               f'(ops.norm_workspace(device, n))')
     arr = (ctypes.c_void_p * world)(*addrs)
     with torch.cuda.device(out.device):
         check(lib().z1_owner_sum_bf16(ctypes.cast(arr, ctypes.c_void_p), world, out.numel(), f32(scale), ptr(out),

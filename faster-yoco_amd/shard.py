@@ -90,7 +90,7 @@ class Zero1ShardOptimizer:
         self._multiply_factor = 1.0
         self._needs_sync = False
         dev = shard.device
-        self._partials = ops.norm_workspace(dev)
+        self._partials = ops.norm_workspace(dev, shard.total if shard.g.dtype == torch.bfloat16 else 0)
         self._factor = torch.ones(1, dtype=torch.float32, device=dev)
         self._norm = torch.zeros(1, dtype=torch.float32, device=dev)
         self._partials_ready = False

@@ -67,10 +67,13 @@ int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* 
  * CEReduce._sum :178-183):
  *   for e in [0,n): acc = 0f; for k = 0..world-1: acc += float(contrib[k][e]); out_avg[e] = bf16(acc * scale)
  * contrib is a HOST array of `world` device pointers (rank order); out_avg may alias one contribution (in place,
- * as OUT does in the reference).  out_sum (nullable) receives acc in fp32.  sumsq_partials (nullable,
- * Z1_NORM_PARTIALS doubles) receives the fused norm partials of the bf16 average for z1_norm_clip. */
+ * as OUT does in the reference).  out_sum (nullable) receives acc in fp32.  sumsq_partials (nullable) is a
+ * workspace of z1_owner_sum_workspace(n) doubles; when given, the norm of the bf16 average is fused in and its
+ * first Z1_NORM_PARTIALS doubles are ready for z1_norm_clip when the call's work completes. */
 int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
                       float* out_sum, double* sumsq_partials, void* stream);
+/* Doubles the fused-norm workspace of z1_owner_sum_bf16 must hold for n elements (negative: error code). */
+int64_t z1_owner_sum_workspace(int64_t n);
 
 /* Multi-tensor sum of squares of the table's gradients (the norm of fairseq utils.clip_grad_norm_ ->
  * apex multi_tensor_l2norm, called at yoco/tasks/zero1_fast.py:150,157): per-workgroup FP64 partials over a fixed

@@ -60,6 +60,8 @@ def test_argument_errors_without_device_work(pkg):
     assert L.z1_scale_up(None, None, None, 4, None) == -1
     assert L.z1_cast_bf16(ctypes.c_void_p(16), ctypes.c_void_p(32), -1, None) == -2
     assert L.z1_table_destroy(None) == 0
+    assert L.z1_owner_sum_workspace(-1) == -2
+    assert [L.z1_owner_sum_workspace(n) for n in (0, 1, 512, 513)] == [2048, 2049, 2049, 2050]
     assert L.z1_table_info(None, None, None, None) == -1
     for code in (0, -1, -2, -3, -4, -5, -6, -7, -99):
         assert L.z1_strerror(code)

@@ -58,7 +58,7 @@ def test_gpu_reproduces_fixture(pkg, dev, path):
     h, mn = hp(f)
     sizes = [int(x) for x in f['sizes']]
     n = sum(sizes)
-    part = ops.norm_workspace(dev)
+    part = ops.norm_workspace(dev, n)
     if 'contribs' in f:
         cs = [configs.to_device_bf16(c, dev) for c in f['contribs']]
         g = torch.empty(n, dtype=torch.bfloat16, device=dev)

@@ -257,7 +257,7 @@ def test_owner_sum_bit_exact(pkg, dev, world):
     ts = [dev_bf16(c, dev) for c in cs]
     out = torch.empty(n, dtype=torch.bfloat16, device=dev)
     osum = torch.empty(n, dtype=torch.float32, device=dev)
-    part = ops.norm_workspace(dev)
+    part = ops.norm_workspace(dev, n)
     ops.owner_sum(ts, out, 1.0 / world, out_sum=osum, partials=part)
     nr = torch.zeros(1, device=dev)
     ops.norm_clip(part, norm_out=nr)
