@@ -47,7 +47,7 @@ def load_traffic(kernel, workload):
 
 def cpu_baseline(shard, cfg, ntensors, contribs, hp, step, threads):
     """Times the PyTorch-CPU restatement (oracle/torch_cpu.py) on the first `ntensors` tensors of the same shard
-    (copied from the GPU buffers), 1 warm-up + median of 3, scaled to the whole shard by parameter count."""
+    (copied from the GPU buffers), 1 warm-up + median of 5, scaled to the whole shard by parameter count."""
     import torch
     sys.path.insert(0, ROOT)
     from oracle import torch_cpu
@@ -63,7 +63,7 @@ def cpu_baseline(shard, cfg, ntensors, contribs, hp, step, threads):
         return [buf[o:o + n] for o, n in zip(shard.offsets[:k], shard.numels[:k])]
 
     times = []
-    for it in range(4):
+    for it in range(6):
         p, m, v = host['p'].clone(), host['m'].clone(), host['v'].clone()
         g = g_host.clone() if g_host is not None else torch.empty(end, dtype=torch.float32)
         p16 = torch.empty(end, dtype=torch.bfloat16)
@@ -79,15 +79,15 @@ def cpu_baseline(shard, cfg, ntensors, contribs, hp, step, threads):
     return {'value': round(ms_sample * shard.numel / n_s, 3), 'unit': 'ms per full-shard step (scaled)',
             'cores': threads, 'kind': 'port',
             'sample': f'first {k} tensors of the same {cfg} shard ({n_s:,} of {shard.numel:,} params), '
-                      f'median of 3 after 1 warm-up = {ms_sample:.1f} ms, scaled by parameter count; '
+                      f'median of 5 after 1 warm-up = {ms_sample:.1f} ms, scaled by parameter count; '
                       f'torch {torch.__version__} CPU, os.cpu_count()={os.cpu_count()}'}
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
-    ap.add_argument('--steps', type=int, default=20)
-    ap.add_argument('--warmup', type=int, default=3)
+    ap.add_argument('--steps', type=int, default=50)
+    ap.add_argument('--warmup', type=int, default=10)
     ap.add_argument('--config', default='c2', choices=sorted(WORKLOADS))
     ap.add_argument('--cpu-sample-tensors', type=int, default=1000)
     ap.add_argument('--no-cpu-baseline', action='store_true')
