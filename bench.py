@@ -83,6 +83,59 @@ def cpu_baseline(shard, cfg, ntensors, contribs, hp, step, threads):
                       f'torch {torch.__version__} CPU, os.cpu_count()={os.cpu_count()}'}
 
 
+def glue_timing(opt, hp, iters=200):
+    """Microseconds per update of the trainer's scalar chain (yoco/tasks/trainer_nosync.py:273-286, :194-197 with
+    zero1_fast.py:150-160) -- multiply_grads factor, norm -> clip, deferred-check flags, "clip" metric -- run as
+    the reference runs it (separate torch ops on the device, flags staged to pinned memory) and as this build runs
+    it (one z1_update_scalars launch).  The norm's partials are computed once beforehand; wall clock over `iters`
+    back-to-back updates, synchronised at the end."""
+    import torch
+    from faster_yoco_amd import ops
+    dev = opt.shard.device
+    ops.grad_sumsq(opt.shard.table, opt._partials)
+    nr = torch.zeros(1, device=dev)
+    ops.norm_clip(opt._partials, norm_out=nr)
+    ss = torch.tensor(16384.0, device=dev)
+    host = torch.zeros(2, dtype=torch.bool, pin_memory=True)
+    c100, c0 = nr.new_tensor(100), nr.new_tensor(0)
+    max_norm = hp['max_norm']
+
+    nr0 = nr.view(())                   # clip_grad_norm_ returns a 0-d tensor
+
+    def reference_ops():
+        denom = torch.where(ss > 0, ss, torch.ones_like(ss))
+        factor = 1.0
+        factor *= 8 / denom
+        sq = nr0.float() ** 2
+        norm = sq.sqrt()
+        grad_norm = factor * norm
+        factor *= (max_norm / (grad_norm + 1e-6)).clamp_(max=1)
+        flags = torch.stack([torch.isfinite(grad_norm).all(), torch.ones((), dtype=torch.bool, device=dev)])
+        host.copy_(flags, non_blocking=True)
+        return torch.where(grad_norm > max_norm, c100, c0)
+
+    flags_d = torch.zeros(2, dtype=torch.uint8, device=dev)
+    gn, fo, cl = (torch.empty(1, device=dev) for _ in range(3))
+    ss1 = ss.reshape(1)
+
+    def fused():
+        ops.update_scalars(opt._partials, sample_size=ss1, numer=8, factor=1.0, max_norm=max_norm, norm_out=nr,
+                           grad_norm_out=gn, factor_out=fo, flags_out=flags_d, clip_log_out=cl)
+        host.copy_(flags_d.view(torch.bool), non_blocking=True)
+
+    out = {}
+    for name, fn in (('reference_torch_ops', reference_ops), ('fused_kernel', fused)):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            fn()
+        torch.cuda.synchronize()
+        out[name] = round((time.perf_counter() - t0) * 1e6 / iters, 1)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -190,6 +243,7 @@ def main():
                      'traffic': load_traffic('adam_cast', cfg),
                      'bytes_per_param': adam_bpp, 'params_per_launch': n},
         'cpu_baseline': cpu,
+        'trainer_scalar_chain_us': glue_timing(opt, hp),
     }
     print(json.dumps(out), flush=True)
 

@@ -30,6 +30,13 @@ class Z1Tensor(ctypes.Structure):
     _fields_ = [('g', _P), ('p', _P), ('m', _P), ('v', _P), ('p16', _P), ('n', _I64)]
 
 
+class Z1UpdateScalars(ctypes.Structure):
+    """``z1_update_scalars``."""
+    _fields_ = [('sample_size', _P), ('numer', _F), ('factor_in', _P), ('factor_value', _F), ('max_norm', _F),
+                ('norm_out', _P), ('grad_norm_out', _P), ('factor_out', _P), ('flags_out', _P),
+                ('clip_log_out', _P)]
+
+
 # name -> (argtypes, restype); every function the header declares
 SIGNATURES = {
     'z1_table_create': ([ctypes.POINTER(Z1Tensor), _I, _I, ctypes.POINTER(_P)], _I),
@@ -40,6 +47,7 @@ SIGNATURES = {
     'z1_grad_sumsq': ([_P, _P, _P], _I),
     'z1_norm_clip': ([_P, _P, _F, _P, _P, _P, _F, _P], _I),
     'z1_clip_factor': ([_P, _P, _F, _P, _P, _F, _P], _I),
+    'z1_update_scalars_run': ([_P, ctypes.POINTER(Z1UpdateScalars), _P], _I),
     'z1_adam_cast': ([_P, _P, _F, _F, _F, _F, _F, _F, _F, _I, _P], _I),
     'z1_scale_up': ([_P, _P, _P, _I64, _P], _I),
     'z1_cast_bf16': ([_P, _P, _I64, _P], _I),

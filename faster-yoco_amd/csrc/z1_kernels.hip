@@ -341,6 +341,39 @@ __global__ __launch_bounds__(kThreads) void norm_clip_kernel(const double* __res
     }
 }
 
+// The trainer's per-update scalars in one kernel (yoco/tasks/trainer_nosync.py:273-286, zero1_fast.py:150-160,
+// and the "clip" metric of trainer_nosync.py:194-197): the sample-size factor, the norm / clip chain, the deferred
+// check flags and the logging constant.
+__global__ __launch_bounds__(kThreads) void update_scalars_kernel(const double* __restrict__ partials,
+                                                                  z1_update_scalars u) {
+    __shared__ double lds[kThreads / kWave];
+    double s = 0.0;
+    for (int i = threadIdx.x; i < Z1_NORM_PARTIALS; i += kThreads) s += partials[i];
+    const double tot = block_sum(s, lds);
+    if (threadIdx.x == 0) {
+        float fac = u.factor_in ? *u.factor_in : u.factor_value;
+        if (u.sample_size) {
+            // multiply_grads(numer / where(ss > 0, ss, 1)): `int / tensor` is reciprocal(tensor) * int in torch
+            const float ss = *u.sample_size;
+            const float denom = (ss > 0.0f) ? ss : 1.0f;
+            const float c = (1.0f / denom) * u.numer;
+            fac = c * fac;
+        }
+        const float nr = (float)__builtin_sqrt(tot);
+        const float sq = nr * nr;
+        const float norm = __builtin_sqrtf(sq);
+        if (u.norm_out) *u.norm_out = nr;
+        const float gn = fac * norm;
+        clip_chain(norm, fac, u.grad_norm_out, u.factor_out, u.max_norm);
+        if (u.flags_out) {
+            const uint32_t b = __float_as_uint(gn) & 0x7fffffffu;
+            u.flags_out[0] = b < 0x7f800000u ? 1 : 0;       // isfinite(grad_norm)
+            u.flags_out[1] = 1;                               // one owner: consistent with itself
+        }
+        if (u.clip_log_out && u.max_norm > 0.0f) *u.clip_log_out = gn > u.max_norm ? 100.0f : 0.0f;
+    }
+}
+
 __global__ void clip_factor_kernel(const float* __restrict__ norm, const float* factor_in, float factor_value,
                                    float* grad_norm_out, float* factor_out, float max_norm) {
     if (threadIdx.x == 0) clip_chain(*norm, factor_in ? *factor_in : factor_value, grad_norm_out, factor_out, max_norm);
@@ -660,6 +693,13 @@ int z1_norm_clip(const double* partials, const float* factor_in, float factor_va
     if (!partials) return Z1_E_NULL;
     hipLaunchKernelGGL(norm_clip_kernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), partials,
                        factor_in, factor_value, norm_out, grad_norm_out, factor_out, max_norm);
+    return launch_status();
+}
+
+int z1_update_scalars_run(const double* partials, const z1_update_scalars* u, void* stream) {
+    if (!partials || !u) return Z1_E_NULL;
+    hipLaunchKernelGGL(update_scalars_kernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), partials,
+                       *u);
     return launch_status();
 }
 

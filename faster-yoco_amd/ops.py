@@ -6,8 +6,8 @@ from collections import OrderedDict
 
 import torch
 
-from ._lib import (Z1_BF16, Z1_F32, Z1_MAX_WORLD, Z1_NORM_PARTIALS, Z1Tensor, check, lib, ptr, require_gpu,
-                   stream_handle)
+from ._lib import (Z1_BF16, Z1_F32, Z1_MAX_WORLD, Z1_NORM_PARTIALS, Z1Tensor, Z1UpdateScalars, check, lib, ptr,
+                   require_gpu, stream_handle)
 
 _GDTYPE = {torch.float32: Z1_F32, torch.bfloat16: Z1_BF16}
 
@@ -150,6 +150,24 @@ def clip_factor(norm, factor=1.0, grad_norm_out=None, factor_out=None, max_norm=
         check(lib().z1_clip_factor(_scalar(norm, 'clip_factor'), fin, fval, _scalar(grad_norm_out, 'clip_factor'),
                                    _scalar(factor_out, 'clip_factor'), f32(max_norm), stream_handle(dev)),
               'z1_clip_factor')
+
+
+def update_scalars(partials, sample_size=None, numer=1.0, factor=1.0, max_norm=0.0, norm_out=None,
+                   grad_norm_out=None, factor_out=None, flags_out=None, clip_log_out=None):
+    """The trainer's per-update scalar chain in one launch (include/yoco_z1.h, z1_update_scalars): optional
+    sample-size factor, norm + clip chain, [finite, consistent] flags (uint8[2]) and the "clip" metric."""
+    require_gpu(partials, 'update_scalars')
+    dev = partials.device
+    fin, fval = _factor_args(factor)
+    if flags_out is not None:
+        require_gpu(flags_out, 'update_scalars')
+        if flags_out.dtype not in (torch.uint8, torch.bool) or flags_out.numel() < 2:
+            raise RuntimeError('update_scalars: flags_out must hold 2 uint8/bool')
+    u = Z1UpdateScalars(_scalar(sample_size, 'update_scalars'), f32(numer), fin, fval, f32(max_norm),
+                        _scalar(norm_out, 'update_scalars'), _scalar(grad_norm_out, 'update_scalars'),
+                        _scalar(factor_out, 'update_scalars'), ptr(flags_out), _scalar(clip_log_out, 'update_scalars'))
+    with torch.cuda.device(dev):
+        check(lib().z1_update_scalars_run(ptr(partials), ctypes.byref(u), stream_handle(dev)), 'z1_update_scalars')
 
 
 def bias_corrections(beta1, beta2, step, bias_correction=1):

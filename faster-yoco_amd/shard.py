@@ -138,6 +138,29 @@ class Zero1ShardOptimizer:
         self._needs_sync = False
         return grad_norm.view(())
 
+    def clip_grad_norm_update(self, max_norm, sample_size=None, numer=1.0, flags_out=None, clip_log_out=None):
+        """multiply_grads(numer / where(sample_size > 0, sample_size, 1)) + clip_grad_norm(max_norm) in one launch,
+        also writing the [finite, consistent] flags and the "clip" metric (yoco/tasks/trainer_nosync.py:273-286,
+        :194-197).  sample_size: 1-element fp32 device tensor or None.  Returns grad_norm (0-d device tensor)."""
+        if not self._partials_ready:
+            ops.grad_sumsq(self.shard.table, self._partials)
+        self._partials_ready = False
+        factor = self._multiply_factor
+        if torch.is_tensor(factor):
+            if not (factor.dtype == torch.float32 and factor.is_cuda and factor.numel() == 1):
+                factor = factor.to(device=self.shard.device, dtype=torch.float32).reshape(1)
+            out = factor
+        else:
+            out = self._factor
+        grad_norm = torch.empty(1, dtype=torch.float32, device=self.shard.device)
+        mn = float(max_norm)
+        ops.update_scalars(self._partials, sample_size=sample_size, numer=numer, factor=factor,
+                           max_norm=mn if mn > 0.0 else 0.0, norm_out=self._norm, grad_norm_out=grad_norm,
+                           factor_out=out, flags_out=flags_out, clip_log_out=clip_log_out)
+        self._multiply_factor = out
+        self._needs_sync = False
+        return grad_norm.view(())
+
     def step(self, closure=None, groups=None):
         """Adam + BF16 over the shard with the gradient factor folded into the gradient load, then factor := 1."""
         self.step_count += 1

@@ -89,6 +89,24 @@ int z1_grad_sumsq(const z1_table* table, double* partials, void* stream);
 int z1_norm_clip(const double* partials, const float* factor_in, float factor_value, float* norm_out,
                  float* grad_norm_out, float* factor_out, float max_norm, void* stream);
 
+/* The trainer's per-update scalar chain, for callers that also own the trainer step (yoco/tasks/
+ * trainer_nosync.py:273-286 with zero1_fast.py:150-160): optional sample-size factor, then the z1_norm_clip chain,
+ * the deferred-check flags and fairseq's "clip" logging value, in one launch.  Every output pointer is nullable. */
+typedef struct z1_update_scalars {
+    const float* sample_size;  /* device fp32 or NULL: factor *= numer / where(ss > 0, ss, 1), computed as torch
+                                  computes `int / tensor`: fp32(fp32(1/denom) * numer) */
+    float numer;               /* the data-parallel numerator (trainer_nosync.py:274) */
+    const float* factor_in;    /* device fp32 factor before the update, or NULL to use factor_value */
+    float factor_value;
+    float max_norm;            /* clip when > 0 */
+    float* norm_out;           /* the fp32 norm of the gradients (clip_grad_norm_'s value) */
+    float* grad_norm_out;      /* factor * norm, as returned by clip_grad_norm */
+    float* factor_out;         /* the clipped factor (may equal factor_in) */
+    uint8_t* flags_out;        /* [isfinite(grad_norm), 1]: the two flags trainer_nosync._Pending.arm stages */
+    float* clip_log_out;       /* 100 if grad_norm > max_norm else 0 (written when max_norm > 0) */
+} z1_update_scalars;
+int z1_update_scalars_run(const double* partials, const z1_update_scalars* u, void* stream);
+
 /* The clip chain entered at `norm` (device fp32), for callers that post-process the norm (aggregate_norm_fn,
  * yoco/tasks/zero1_fast.py:153-160): grad_norm = factor*norm; clip as above.  Factor arguments as above. */
 int z1_clip_factor(const float* norm, const float* factor_in, float factor_value, float* grad_norm_out,

@@ -48,6 +48,7 @@ def lib():
         L.oracle_sumsq_bf16.restype = ctypes.c_double
         L.oracle_norm_clip.argtypes = [ctypes.c_double, _F, _F, _P]
         L.oracle_clip_factor.argtypes = [_F, _F, _F, _P]
+        L.oracle_update_scalars.argtypes = [ctypes.c_double, _I, _F, _F, _F, _F, _P]
         L.oracle_bias_corrections.argtypes = [ctypes.c_double, ctypes.c_double, _I64, _I, _P]
         L.oracle_adam_cast.argtypes = [_P, _I, _P, _P, _P, _P, _I64, _F, _I, _F, _F, _F, _F, _F, _F, _F, _I]
         L.oracle_greedy_partition.argtypes = [_P, _I, _I, _P, _P]
@@ -139,6 +140,18 @@ def clip_factor(norm, factor=1.0, max_norm=1.0):
     return out[0], out[1]
 
 
+def update_scalars(sumsq_value, sample_size=None, numer=1.0, factor=1.0, max_norm=1.0):
+    """trainer_nosync.py:273-285 + zero1_fast.py:150-160 (one owner) + the "clip" metric (:194-197).
+    Returns dict(norm, grad_norm, factor, finite, consistent, clip_log) as np.float32 / bool / None."""
+    out = np.empty(6, dtype=np.float32)
+    lib().oracle_update_scalars(float(sumsq_value), int(sample_size is not None),
+                                float(np.float32(0.0 if sample_size is None else sample_size)),
+                                float(np.float32(numer)), float(np.float32(factor)), float(np.float32(max_norm)),
+                                _ptr(out))
+    return dict(norm=out[0], grad_norm=out[1], factor=out[2], finite=bool(out[3]), consistent=bool(out[4]),
+                clip_log=None if out[5] < 0 else out[5])
+
+
 def bias_corrections(beta1, beta2, step, bias_correction=1):
     """fused_adam_cast.py:58-60.  Returns (bc1, bc2) as np.float32."""
     out = np.empty(2, dtype=np.float32)
@@ -189,4 +202,4 @@ def ulp_diff_f32(a, b):
 
 
 __all__ = ['bf16_rne', 'bf16_to_f32', 'owner_sum', 'sum_slots', 'scale_up', 'sumsq', 'norm_clip', 'clip_factor',
-           'bias_corrections', 'adam_cast', 'greedy_partition', 'ulp_diff_f32', 'build', 'lib']
+           'update_scalars', 'bias_corrections', 'adam_cast', 'greedy_partition', 'ulp_diff_f32', 'build', 'lib']

@@ -122,6 +122,29 @@ void oracle_norm_clip(double sumsq, float factor, float max_norm, float* out) {
     out[2] = f;
 }
 
+/*
+ * trainer_nosync.py:273-282 then zero1_fast.py:150-160 (one owner), plus the flags of trainer_nosync.py:285 and the
+ * "clip" metric of :194-197.  has_ss: multiply the factor by numer / where(ss > 0, ss, 1) first (torch computes
+ * `int / tensor` as reciprocal(tensor) * int).  out: [n_r, grad_norm, factor, finite, consistent, clip_log].
+ */
+void oracle_update_scalars(double sumsq, int has_ss, float ss, float numer, float factor, float max_norm,
+                           float* out) {
+    float fac = factor;
+    if (has_ss) {
+        float denom = (ss > 0.0f) ? ss : 1.0f;
+        float c = (1.0f / denom) * numer;
+        fac = c * fac;
+    }
+    float chain[3];
+    oracle_norm_clip(sumsq, fac, max_norm, chain);
+    out[0] = chain[0];
+    out[1] = chain[1];
+    out[2] = chain[2];
+    out[3] = isfinite(chain[1]) ? 1.0f : 0.0f;
+    out[4] = 1.0f;
+    out[5] = (max_norm > 0.0f) ? (chain[1] > max_norm ? 100.0f : 0.0f) : -1.0f;
+}
+
 /* Same chain entered at `norm` (after sqrt(sq)), for the aggregate_norm_fn path. out[0]=grad_norm, out[1]=factor */
 void oracle_clip_factor(float norm, float factor, float max_norm, float* out) {
     float gn = factor * norm;

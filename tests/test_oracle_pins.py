@@ -156,6 +156,39 @@ def test_norm_clip_chain_matches_torch_expressions(factor):
             assert bits32(o_gn) == bits32(gn) and bits32(o_f) == bits32(f), (nr, max_norm)
 
 
+def _torch_trainer_scalars(nr, ss, numer, max_norm):
+    """yoco/tasks/trainer_nosync.py:273-285 and :194-197 around zero1_fast.py:150-160, literally, on torch CPU."""
+    sample_size = torch.tensor(ss, dtype=torch.float32)
+    denom = torch.where(sample_size > 0, sample_size, torch.ones_like(sample_size))
+    factor = 1.0
+    factor *= numer / denom                                   # multiply_grads
+    sq = torch.tensor(nr, dtype=torch.float32).float() ** 2
+    norm = sq.sqrt()
+    grad_norm = factor * norm
+    if max_norm > 0.0:
+        factor *= (max_norm / (grad_norm + 1e-6)).clamp_(max=1)
+    finite = bool(torch.isfinite(grad_norm).all())
+    clip = (torch.where(grad_norm > max_norm, grad_norm.new_tensor(100), grad_norm.new_tensor(0)).item()
+            if max_norm > 0 else None)
+    return np.float32(grad_norm.item()), np.float32(factor.item()), finite, clip
+
+
+def test_update_scalars_match_trainer_torch_expressions():
+    rng = np.random.default_rng(8)
+    norms = list(np.float32(10.0 ** rng.uniform(-6, 6, 60))) + [np.float32(0.0), np.float32(np.inf)]
+    for nr in norms:
+        for ss in (16384.0, 2048.0, 1.0, 0.0, -3.0, 12345.0):
+            for numer in (8, 1):
+                for max_norm in (1.0, 0.0):
+                    gn, f, finite, clip = _torch_trainer_scalars(float(nr), ss, numer, max_norm)
+                    o = oracle.update_scalars(float(nr) ** 2, ss, numer, 1.0, max_norm)
+                    assert bits32(o['grad_norm']) == bits32(gn) and bits32(o['factor']) == bits32(f)
+                    assert o['finite'] == finite and o['consistent']
+                    assert o['clip_log'] == clip
+    o = oracle.update_scalars(float('nan'), float('nan'), 8, 1.0, 1.0)
+    assert not o['finite'] and np.isnan(o['factor'])
+
+
 def test_norm_clip_nan_propagates():
     o_nr, o_gn, o_f = oracle.norm_clip(float('nan'), 1.0, 1.0)
     assert np.isnan(o_nr) and np.isnan(o_gn) and np.isnan(o_f)
