@@ -136,6 +136,37 @@ def glue_timing(opt, hp, iters=200):
     return out
 
 
+def embedding_timing(dev, reps=20):
+    """The embedding owner's gradient at the recipe's size (8 ranks x 2048 token rows of 3072, vocabulary 100,288):
+    torch's aten.embedding_dense_backward + x 1/world as the reference runs it, against this build's fused kernel;
+    HIP events on the current stream, milliseconds per call."""
+    import torch
+    from faster_yoco_amd import embedding
+    R, D, V = 8 * 2048, 3072, 100288
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    ids = torch.randint(0, V, (R,), device=dev, generator=gen)
+    g = (torch.randn(R, D, device=dev, generator=gen) * 1e-2).to(torch.bfloat16)
+    out = torch.empty(V, D, dtype=torch.bfloat16, device=dev)
+    res = {}
+    for name, fn in (('aten_embedding_dense_backward', lambda: torch.ops.aten.embedding_dense_backward(
+                          g, ids, V, -1, False).mul_(1.0 / 8)),
+                     ('z1_embedding_backward', lambda: embedding.owner_embedding_grad(g, ids, V, -1, 8))):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = round(e0.elapsed_time(e1) / reps, 4)
+    del out
+    res.update(rows=R, dim=D, vocab=V, bytes_written=V * D * 2)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -244,6 +275,7 @@ def main():
                      'bytes_per_param': adam_bpp, 'params_per_launch': n},
         'cpu_baseline': cpu,
         'trainer_scalar_chain_us': glue_timing(opt, hp),
+        'owner_embedding_grad_ms': embedding_timing(dev),
     }
     print(json.dumps(out), flush=True)
 

@@ -9,9 +9,10 @@ Modules
     fused_adam_cast  drop-in for yoco/tasks/fused_adam_cast.py (FusedAdamCast, scale_up)
     zero1_fast       drop-in for yoco/tasks/zero1_fast.py (clip_grad_norm / step / zero_grad patches, layout)
     ce_reduce        drop-in for the owner-sum kernel of yoco/models/decoder/ce_reduce.py (_sum_slots, _sum)
+    embedding        drop-in for the owner's token-embedding gradient (aten embedding_dense_backward + 1/world)
     trainer_glue     the optimizer part of trainer_nosync.train_step: one-launch scalar chain + deferred checks
     configs          the benchmark/parity workloads (tensor lists and synthetic inputs)
 """
 from . import _lib, ops  # noqa: F401
 
-__all__ = ['ops', 'shard', 'fused_adam_cast', 'zero1_fast', 'ce_reduce', 'configs', 'layout', 'trainer_glue']
+__all__ = ['ops', 'shard', 'fused_adam_cast', 'zero1_fast', 'ce_reduce', 'configs', 'layout', 'trainer_glue', 'embedding']

@@ -9,7 +9,7 @@ CSRC = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(CSRC)
 ROOT = os.path.dirname(PKG)
 INCLUDE = os.path.join(ROOT, 'include')
-SOURCES = [os.path.join(CSRC, 'z1_kernels.hip')]
+SOURCES = [os.path.join(CSRC, 'z1_kernels.hip'), os.path.join(CSRC, 'z1_embedding.hip')]
 OUTPUT = os.path.join(PKG, 'libyoco_z1.so')
 ARCH = os.environ.get('YOCO_Z1_ARCH', 'gfx950')
 

@@ -125,6 +125,18 @@ int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n,
 /* p16[i] = bf16(p32[i]) (the leftover casts of yoco/tasks/zero1_fast.py:198-209). */
 int z1_cast_bf16(const float* p32, uint16_t* p16, int64_t n, void* stream);
 
+/* The embedding owner's token-embedding gradient: out[V x D] (bf16) = torch.ops.aten.embedding_dense_backward(
+ * grad[R x D] (bf16), ids[R] (int64), V, padding_idx, False) with the reference's x 1/world
+ * (yoco/models/decoder/layer_graphs.py:87-93: scale after, scale_mode 2; yoco/models/decoder/ce_reduce.py:226-231:
+ * rows scaled first, scale_mode 1; 0: no scale).  Same order as aten's sort-based GPU path: each id's occurrences
+ * in position order, fp32 partial sums over runs of 10, partials summed in order, one bf16 rounding.  Every row of
+ * out is written (rows without occurrences, padding_idx and ids outside [0, V) give zeros).  workspace: device
+ * memory of z1_embedding_backward_workspace(R, V) bytes. */
+int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, int64_t D, int64_t V,
+                          int64_t padding_idx, float scale, int scale_mode, uint16_t* out, void* workspace,
+                          int64_t workspace_bytes, void* stream);
+int64_t z1_embedding_backward_workspace(int64_t R, int64_t V);
+
 /* Text for a return code (negative: argument errors; positive: hipError_t). */
 const char* z1_strerror(int code);
 

@@ -52,6 +52,7 @@ def lib():
         L.oracle_bias_corrections.argtypes = [ctypes.c_double, ctypes.c_double, _I64, _I, _P]
         L.oracle_adam_cast.argtypes = [_P, _I, _P, _P, _P, _P, _I64, _F, _I, _F, _F, _F, _F, _F, _F, _F, _I]
         L.oracle_greedy_partition.argtypes = [_P, _I, _I, _P, _P]
+        L.oracle_embedding_backward.argtypes = [_P, _P, _I64, _I64, _I64, _I64, _F, _I, _P]
         _LIB = L
     return _LIB
 
@@ -183,6 +184,19 @@ def adam_cast(g, p, m, v, *, lr, beta1, beta2, eps, weight_decay, step, mode=1, 
     return p, m, v, p16
 
 
+def embedding_backward(ids, grad16, num_weights, padding_idx=-1, scale=None, scale_first=False):
+    """aten.embedding_dense_backward's sort-path order (+ the reference's optional 1/world), see z1_oracle.c.
+    ids: int64 [R]; grad16: uint16 bf16 bits [R, D].  Returns uint16 [V, D]."""
+    ids = _c(np.asarray(ids, dtype=np.int64), np.int64)
+    g = _c(grad16, np.uint16)
+    R, D = g.shape
+    out = np.empty((num_weights, D), dtype=np.uint16)
+    mode = 0 if scale is None else (1 if scale_first else 2)
+    lib().oracle_embedding_backward(_ptr(ids), _ptr(g), R, D, num_weights, padding_idx,
+                                    float(np.float32(1.0 if scale is None else scale)), mode, _ptr(out))
+    return out
+
+
 def greedy_partition(numels, world):
     """zero1_fast.py:61-65.  Returns (owner list, per-rank sizes)."""
     nums = np.asarray(numels, dtype=np.int64)
@@ -202,4 +216,4 @@ def ulp_diff_f32(a, b):
 
 
 __all__ = ['bf16_rne', 'bf16_to_f32', 'owner_sum', 'sum_slots', 'scale_up', 'sumsq', 'norm_clip', 'clip_factor',
-           'update_scalars', 'bias_corrections', 'adam_cast', 'greedy_partition', 'ulp_diff_f32', 'build', 'lib']
+           'update_scalars', 'bias_corrections', 'adam_cast', 'embedding_backward', 'greedy_partition', 'ulp_diff_f32', 'build', 'lib']

@@ -209,6 +209,40 @@ void oracle_adam_cast(const void* g, int g_bf16, float* p, float* m, float* v, u
     }
 }
 
+/*
+ * torch.ops.aten.embedding_dense_backward(grad[R x D], ids[R], V, padding_idx, False) as its sort-based GPU path
+ * sums (called at yoco/models/decoder/layer_graphs.py:92 and ce_reduce.py:230): for each id t, its occurrences in
+ * position order, fp32 partial sums over runs of 10, the partials summed in order, one bf16 rounding; padding rows
+ * and ids outside [0, V) give zero rows.  scale_mode 1: each grad element first rounded to bf16(g * scale);
+ * 2: the bf16 result multiplied by scale and rounded again.  Brute force over t (test sizes only).
+ */
+void oracle_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, int64_t D, int64_t V,
+                               int64_t padding_idx, float scale, int scale_mode, uint16_t* out) {
+    for (int64_t t = 0; t < V; ++t) {
+        for (int64_t d = 0; d < D; ++d) {
+            float acc = 0.0f, part = 0.0f;
+            int64_t k = 0;
+            for (int64_t r = 0; r < R; ++r) {
+                if (ids[r] != t) continue;
+                float x = bf16_to_f32(grad[r * D + d]);
+                if (scale_mode == 1) x = bf16_to_f32(oracle_bf16_rne(x * scale));
+                part = part + x;
+                if (++k == 10) {
+                    acc = acc + part;
+                    part = 0.0f;
+                    k = 0;
+                }
+            }
+            if (k) acc = acc + part;
+            uint16_t o = oracle_bf16_rne(acc);
+            if (scale_mode == 2) o = oracle_bf16_rne(bf16_to_f32(o) * scale);
+            int none = 1;
+            for (int64_t r = 0; r < R && none; ++r) none = ids[r] != t;
+            out[t * D + d] = (t == padding_idx || none) ? 0 : o;
+        }
+    }
+}
+
 /* zero1_fast.py:61-65: params in order, each to the rank with the smallest running total (first such rank). */
 void oracle_greedy_partition(const int64_t* numel, int nparam, int world, int32_t* owner, int64_t* sizes) {
     for (int r = 0; r < world; ++r) sizes[r] = 0;

@@ -1,0 +1,65 @@
+"""The owner's token-embedding gradient on the GPU, against torch's own aten.embedding_dense_backward on the same
+device (the routine the reference calls, yoco/models/decoder/layer_graphs.py:92, ce_reduce.py:230) and against the
+oracle.  aten takes its sort-based path for more than 3072 indices; that is the order restated here (bit-exact)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def zipf_ids(rng, R, V, a=1.2):
+    ids = rng.zipf(a, R) - 1
+    return np.where(ids < V, ids, rng.integers(0, V, R)).astype(np.int64)
+
+
+def bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+@pytest.mark.parametrize('padding_idx', [-1, 1])
+@pytest.mark.parametrize('D', [3072, 200])
+def test_matches_aten_sort_path(pkg, dev, padding_idx, D):
+    from faster_yoco_amd import embedding
+    rng = np.random.default_rng(D + padding_idx)
+    R, V = 8 * 2048, 100288
+    ids = torch.from_numpy(zipf_ids(rng, R, V)).to(dev)
+    assert int((ids == 0).sum()) > 100                       # long runs: many partials of 10
+    g = (torch.randn(R, D, device=dev) * 1e-2).to(torch.bfloat16)
+    ref = torch.ops.aten.embedding_dense_backward(g, ids, V, padding_idx, False)
+    got = embedding.embedding_dense_backward(g, ids, V, padding_idx)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(got), bits(ref))
+    # the reference's two 1/world placements
+    ref2 = torch.ops.aten.embedding_dense_backward(g, ids, V, padding_idx, False).mul_(1.0 / 8)
+    got2 = embedding.owner_embedding_grad(g, ids, V, padding_idx, 8)
+    ref3 = torch.ops.aten.embedding_dense_backward(g.clone().mul_(1.0 / 8), ids, V, padding_idx, False)
+    got3 = embedding.ce_owner_embedding_grad(g, ids, V, padding_idx, 8)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(got2), bits(ref2)) and np.array_equal(bits(got3), bits(ref3))
+
+
+def test_matches_oracle_and_edge_cases(pkg, dev):
+    from faster_yoco_amd import embedding
+    rng = np.random.default_rng(3)
+    R, V, D = 4000, 300, 13                                   # D % 8 != 0: the element path
+    ids = zipf_ids(rng, R, V, 1.5)
+    ids[:4] = [-5, V, V + 7, 2 ** 40]                         # outside [0, V): contribute nothing
+    g16 = oracle.bf16_rne((rng.standard_normal((R, D)) * 1e-2).astype(np.float32))
+    for pad, scale, first in ((-1, None, False), (3, 0.125, False), (0, 0.125, True)):
+        exp = oracle.embedding_backward(ids, g16, V, padding_idx=pad, scale=scale, scale_first=first)
+        gt = torch.from_numpy(g16.view(np.int16)).to(dev).view(torch.bfloat16)
+        got = embedding.embedding_dense_backward(gt, torch.from_numpy(ids).to(dev), V, pad, scale=scale,
+                                                 scale_first=first)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(got), exp)
+    # no rows at all: a zero table; a preexisting out buffer is fully overwritten
+    out = torch.full((V, 16), 7.0, dtype=torch.bfloat16, device=dev)
+    embedding.embedding_dense_backward(torch.zeros(0, 16, dtype=torch.bfloat16, device=dev),
+                                       torch.zeros(0, dtype=torch.int64, device=dev), V, -1, out=out)
+    torch.cuda.synchronize()
+    assert not out.float().abs().sum().item()
+    with pytest.raises(RuntimeError, match='scale_grad_by_freq'):
+        embedding.embedding_dense_backward(gt, torch.from_numpy(ids).to(dev), V, -1, True)

@@ -318,3 +318,42 @@ def test_greedy_partition_known_answer(pkg):
         nums = rng.integers(1, 10_000, rng.integers(1, 60)).tolist()
         w = int(rng.integers(1, 9))
         assert layout.greedy_partition(nums, w) == oracle.greedy_partition(nums, w)
+
+
+# --------------------------------------------------------------------------------------------- embedding grad
+def test_embedding_backward_exact_cases():
+    rng = np.random.default_rng(14)
+    V, D = 50, 6
+    ids = rng.permutation(V)[:30].astype(np.int64)          # no repeats: rows are copied exactly
+    g = oracle.bf16_rne(rng.standard_normal((30, D)).astype(np.float32))
+    out = oracle.embedding_backward(ids, g, V, padding_idx=int(ids[3]))
+    exp = np.zeros((V, D), np.uint16)
+    exp[ids] = g
+    exp[ids[3]] = 0
+    assert np.array_equal(out, exp)
+    # small-integer values: every partial and total is exact, so the result is the plain sum in any order
+    ids = rng.integers(0, 8, 500).astype(np.int64)
+    ids[:5] = [-1, 8, 9, 100, -7]                            # outside [0, V): ignored
+    vals = rng.integers(-3, 4, (500, D)).astype(np.float32)
+    out = oracle.embedding_backward(ids, oracle.bf16_rne(vals), 8)
+    exp = np.zeros((8, D), np.float32)
+    np.add.at(exp, ids[5:], vals[5:])
+    assert np.array_equal(out, torch_bf16_bits(exp))
+    # the 1/world scale: before or after, exact for a power of two
+    a = oracle.embedding_backward(ids, oracle.bf16_rne(vals), 8, scale=0.125)
+    b = oracle.embedding_backward(ids, oracle.bf16_rne(vals), 8, scale=0.125, scale_first=True)
+    assert np.array_equal(a, b) and np.array_equal(a, torch_bf16_bits(exp * 0.125))
+
+
+def test_embedding_backward_sums_in_runs_of_ten():
+    """1 + 2^-8 followed by 18 x 2^-24: added one by one the tiny values are lost (ties to even) and the bf16 result
+    is the tie 1 + 2^-8 -> 1.0; summed as aten does (partials over runs of 10 occurrences) the second run keeps
+    10 x 2^-24 and the result rounds up to 1 + 2^-7."""
+    vals = [1.0, 2.0 ** -8] + [2.0 ** -24] * 18
+    g = oracle.bf16_rne(np.array(vals, np.float32).reshape(-1, 1))
+    out = oracle.embedding_backward(np.zeros(len(vals), np.int64), g, 1)
+    assert out[0, 0] == 0x3F81
+    seq = np.float32(0.0)
+    for v in vals:
+        seq = np.float32(seq + np.float32(v))
+    assert torch_bf16_bits(np.array([seq], np.float32))[0] == 0x3F80
