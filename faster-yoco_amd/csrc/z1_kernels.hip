@@ -753,14 +753,15 @@ int64_t z1_owner_sum_workspace(int64_t n) {
 
 int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
                       float* out_sum, double* sumsq_partials, void* stream) {
-    if (!contrib || !out_avg) return Z1_E_NULL;
+    if (!contrib) return Z1_E_NULL;
     if (world < 1 || world > Z1_MAX_WORLD) return Z1_E_WORLD;
     if (n < 0) return Z1_E_SIZE;
+    if (n > 0 && !out_avg) return Z1_E_NULL;               // empty inputs may carry NULL data pointers
     Srcs srcs;
     memset(&srcs, 0, sizeof(srcs));
     int vec = aligned(out_avg, 16) && (!out_sum || aligned(out_sum, 16));
     for (int k = 0; k < world; ++k) {
-        if (!contrib[k]) return Z1_E_NULL;
+        if (n > 0 && !contrib[k]) return Z1_E_NULL;
         srcs.p[k] = contrib[k];
         if (!aligned(contrib[k], 16)) vec = 0;
     }
@@ -783,9 +784,9 @@ int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, floa
 }
 
 int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n, void* stream) {
-    if (!g16 || !g32 || !factor) return Z1_E_NULL;
     if (n < 0) return Z1_E_SIZE;
     if (n == 0) return Z1_OK;
+    if (!g16 || !g32 || !factor) return Z1_E_NULL;
     int dev = 0, grid = 0;
     int rc = current_device(&dev);
     if (rc) return rc;
@@ -798,9 +799,9 @@ int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n,
 }
 
 int z1_cast_bf16(const float* p32, uint16_t* p16, int64_t n, void* stream) {
-    if (!p32 || !p16) return Z1_E_NULL;
     if (n < 0) return Z1_E_SIZE;
     if (n == 0) return Z1_OK;
+    if (!p32 || !p16) return Z1_E_NULL;
     int dev = 0, grid = 0;
     int rc = current_device(&dev);
     if (rc) return rc;

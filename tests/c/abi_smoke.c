@@ -1,0 +1,22 @@
+/* Plain-C consumer of include/yoco_z1.h: compiled with gcc -std=c11 and linked against libyoco_z1.so by
+ * tests/test_abi_host.py.  Without a GPU it only exercises calls that return before any device work. */
+#include <stdio.h>
+#include <string.h>
+
+#include "yoco_z1.h"
+
+int main(void) {
+    z1_table* t = 0;
+    int bad = 0;
+    bad |= z1_table_create(0, -1, Z1_F32, &t) != Z1_E_SIZE;
+    bad |= z1_table_create(0, 0, 7, &t) != Z1_E_DTYPE;
+    bad |= z1_owner_sum_workspace(513) != Z1_NORM_PARTIALS + 2;
+    bad |= z1_adam_cast(0, 0, 0.f, 0.f, 0.f, 0.f, 1.f, 1.f, 0.f, 1, 0) != Z1_E_NULL;
+    bad |= strlen(z1_strerror(Z1_E_WORKSPACE)) == 0;
+    z1_update_scalars u;
+    memset(&u, 0, sizeof(u));
+    bad |= z1_update_scalars_run(0, &u, 0) != Z1_E_NULL;
+    bad |= z1_embedding_backward_workspace(-1, 10) != Z1_E_SIZE;
+    printf("%s\n", bad ? "FAIL" : "ok");
+    return bad;
+}

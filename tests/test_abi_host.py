@@ -46,6 +46,11 @@ def test_argument_errors_without_device_work(pkg):
     row = (_lib.Z1Tensor * 1)(_lib.Z1Tensor(16, None, None, None, None, -5))
     assert L.z1_table_create(row, 1, 0, ctypes.byref(h)) == -2
     assert L.z1_owner_sum_bf16(None, 8, 10, 0.125, None, None, None, None) == -1
+    nulls = (ctypes.c_void_p * 2)(None, None)
+    assert L.z1_owner_sum_bf16(ctypes.cast(nulls, ctypes.c_void_p), 2, 10, 0.5, ctypes.c_void_p(32), None, None,
+                               None) == -1
+    assert L.z1_scale_up(None, None, None, 0, None) == 0                      # empty: a no-op whatever the pointers
+    assert L.z1_cast_bf16(None, None, 0, None) == 0
     arr = (ctypes.c_void_p * 1)(16)
     assert L.z1_owner_sum_bf16(ctypes.cast(arr, ctypes.c_void_p), 0, 10, 1.0, ctypes.c_void_p(32), None, None,
                                None) == -4
@@ -59,6 +64,7 @@ def test_argument_errors_without_device_work(pkg):
     assert L.z1_clip_factor(None, None, 1.0, None, None, 1.0, None) == -1
     assert L.z1_scale_up(None, None, None, 4, None) == -1
     assert L.z1_cast_bf16(ctypes.c_void_p(16), ctypes.c_void_p(32), -1, None) == -2
+    assert L.z1_cast_bf16(None, None, 4, None) == -1
     assert L.z1_table_destroy(None) == 0
     assert L.z1_owner_sum_workspace(-1) == -2
     assert [L.z1_owner_sum_workspace(n) for n in (0, 1, 512, 513)] == [2048, 2049, 2049, 2050]
@@ -131,3 +137,17 @@ def test_layout_place_params_cpu(pkg):
         assert torch.equal(p.data, b) and st['owner'][id(p)] == r
         off = (p.data.data_ptr() - st['flat'].data_ptr()) // 4
         assert r * st['seg'] <= off < (r + 1) * st['seg']
+
+
+def test_header_is_plain_c_and_links(pkg, tmp_path):
+    """include/yoco_z1.h compiles as C11 with gcc and a C program links and runs against libyoco_z1.so (argument
+    errors only: no device work)."""
+    import subprocess
+    from faster_yoco_amd import _lib
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    exe = tmp_path / 'abi_smoke'
+    subprocess.run(['gcc', '-std=c11', '-Wall', '-Werror', '-I', os.path.join(ROOT, 'include'),
+                    os.path.join(ROOT, 'tests', 'c', 'abi_smoke.c'), '-L', libdir, '-l:libyoco_z1.so',
+                    f'-Wl,-rpath,{libdir}', '-o', str(exe)], check=True)
+    res = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0 and res.stdout.strip() == 'ok', res.stdout + res.stderr
