@@ -199,3 +199,68 @@ def test_ce_reduce_sum_installed(pkg, dev):
             oracle.sum_slots(S, exp, G, a, b, R, 1.0 / W, W)
         torch.cuda.synchronize()
         assert np.array_equal(bits(ce.out), exp)
+
+
+def test_zero1_fast_measured_switch_set_with_placed_params(pkg, dev):
+    """scripts/configs/faster.env's optimizer switches (ZERO1_FAST, ALLGATHER, PARAM_VIEWS, PARAM_ALLREDUCE +
+    GRAD_REDUCE_OWNER, Z1_ONE_PASS, Z1_SCALE_KERNEL, FUSED_ADAM) with torch.distributed initialised (gloo, one
+    rank): _place_params puts the parameters into the flat BF16 buffer (zero1_fast.py:52-75), _setup checks the
+    placement against the OSS partition (:103-118), and the update writes the BF16 copy straight into the placed
+    parameters."""
+    import torch.distributed as dist
+    from faster_yoco_amd import layout, zero1_fast
+    if dist.is_initialized():
+        pytest.skip('a process group already exists')
+    dist.init_process_group('gloo', init_method='tcp://127.0.0.1:29531', rank=0, world_size=1)
+    try:
+        zero1_fast.configure(ENABLED=True, ALLGATHER=True, PARAM_VIEWS=True, REDUCE_OWNER=True, ONE_PASS=True,
+                             SCALE_KERNEL=True, FUSED_ADAM=True, FOLD_SCALE=True)
+        zero1_fast._PLACED.clear()
+        module = torch.nn.Module()
+        for i, p in enumerate(bf16_params(dev, 7)):
+            module.register_parameter(f'w{i}', p)
+        zero1_fast._place_params(module)
+        params = list(module.parameters())
+        flat = zero1_fast._PLACED['flat']
+        owner, where, seg = layout.segments([p.numel() for p in params], 1)
+        assert zero1_fast._PLACED['seg'] == seg
+        for p, off in zip(params, where):
+            assert p.data_ptr() == flat.data_ptr() + off * 2
+
+        class Mixin(fakes.FakeMixin):
+            pass
+
+        zero1_fast._ORIG.clear()
+        zero1_fast.install(Mixin)
+
+        class Opt(Mixin, fakes.FakeFP16Optimizer):
+            pass
+
+        opt = Opt(params, lr=HP['lr'], betas=(HP['beta1'], HP['beta2']), eps=HP['eps'],
+                  weight_decay=HP['weight_decay'])
+        state = [(p.detach().float().cpu().numpy().ravel().copy(), np.zeros(p.numel(), np.float32),
+                  np.zeros(p.numel(), np.float32)) for p in params]
+        for step in (1, 2):
+            set_grads(params, 40 + step)
+            grads16 = [bits(p.grad).ravel().copy() for p in params]
+            opt.multiply_grads(8 / torch.tensor(16384.0, device=dev))
+            opt.clip_grad_norm(1.0)
+            fac = float(opt._multiply_factor.item())
+            opt.step()
+            torch.cuda.synchronize()
+            assert opt._z1['placed']
+            for i, p in enumerate(params):
+                po, mo, vo, p16 = oracle.adam_cast(grads16[i], *state[i], step=step, factor=fac, **HP)
+                assert np.array_equal(bits(p).ravel(), p16), i            # the placed view itself was written
+                assert np.array_equal(bits(opt.fp32_params[i]).ravel(), po.view(np.uint32)), i
+                state[i] = (po, mo, vo)
+            opt.zero_grad()
+        # a parameter moved out of its slot is refused, as the reference refuses it
+        opt2 = Opt(params)
+        params[0].data = params[0].data.clone()
+        with pytest.raises(RuntimeError, match='not at its slot'):
+            opt2.clip_grad_norm(1.0)
+    finally:
+        zero1_fast.configure(ENABLED=False, ALLGATHER=False, PARAM_VIEWS=False, REDUCE_OWNER=False)
+        zero1_fast._PLACED.clear()
+        dist.destroy_process_group()
