@@ -18,7 +18,13 @@
 //   * The norm uses the same table and a FIXED grid (Z1_NORM_PARTIALS workgroups of 4 waves; workgroup b takes
 //     chunks 4b..4b+3, then 4(b+G).., i.e. 1024 contiguous elements per step), FP64 accumulation of the exact
 //     squares per lane, a wave64 xor-butterfly and a fixed-order LDS stage: its bits do not depend on timing, on
-//     the device's CU count or on the run.  This read pattern measured 7.0 TB/s on MI355X.
+//     the device's CU count or on the run.  Measured 0.27 ms for the 1.72 GB gradient (6.4 TB/s); one wave per
+//     chunk with hardware dispatch (0.40 ms), 4-chunk workgroups with hardware dispatch (0.34 ms) and 2-8 loads
+//     in flight per wave (0.28-0.31 ms) were all slower.
+//   * MALL reuse between passes: the pass before Adam (the norm, or the owner sum that writes the BF16 average)
+//     touches the last kMallKeepBytes of the gradient with ordinary, allocating accesses, and Adam walks the
+//     chunks from the last one, so its first gradient reads hit the 256 MB MALL (measured 2.05 vs 2.10 ms for
+//     Adam on the C2 shard; 128-512 MB kept, or everything, measured the same or slower).
 //   * No atomics anywhere; nothing but vector memory instructions write memory.
 //
 // Numerics follow the header: one rounding per fp32 operation, explicit FMAs where the reference has them,
@@ -47,6 +53,10 @@ constexpr int kAdamWaves = 1;                                 // chunks (one per
 constexpr int kVec = 4;                                       // fp32 lanes of one 128-bit access
 constexpr int kGroups = 1;                                    // 128-bit groups per lane per array and chunk
 constexpr int64_t kChunk = (int64_t)kWave * kVec * kGroups;   // elements per chunk: one wave's share
+// The norm pass reads (the owner sum writes) the last kMallKeepBytes of the gradient with ordinary, allocating
+// accesses, so that they are still in the 256 MB MALL when the Adam pass -- which walks the chunks from the end --
+// reads them again.
+constexpr int64_t kMallKeepBytes = 256ll << 20;
 constexpr int kMaxDevices = 64;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -84,8 +94,18 @@ __device__ __forceinline__ T ld(const T* p) {
 }
 
 template <typename T>
+__device__ __forceinline__ T ld_keep(const T* p) {       // ordinary load: allocates in L2 and the MALL
+    return *(const Z1_GLOBAL T*)p;
+}
+
+template <typename T>
 __device__ __forceinline__ void st(T* p, T x) {
     __builtin_nontemporal_store(x, (Z1_GLOBAL T*)p);
+}
+
+template <typename T>
+__device__ __forceinline__ void st_keep(T* p, T x) {     // ordinary store: allocates in L2 and the MALL
+    *(Z1_GLOBAL T*)p = x;
 }
 
 // Chunk of workgroup b: undoes the round-robin dispatch over the 8 XCDs (workgroup b runs on XCD b mod 8), so that
@@ -139,6 +159,13 @@ __device__ __forceinline__ f4 load_g4(const void* g, int64_t i) {
 }
 
 template <int GDT>
+__device__ __forceinline__ f4 load_g4_keep(const void* g, int64_t i) {
+    if (GDT == Z1_F32) return ld_keep(reinterpret_cast<const f4*>(static_cast<const float*>(g) + i));
+    const u2 h = ld_keep(reinterpret_cast<const u2*>(static_cast<const uint16_t*>(g) + i));
+    return f4{bf16_lo(h.x), bf16_hi(h.x), bf16_lo(h.y), bf16_hi(h.y)};
+}
+
+template <int GDT>
 __device__ __forceinline__ float load_g1(const void* g, int64_t i) {
     if (GDT == Z1_F32) return static_cast<const float*>(g)[i];
     return bf16_to_f32(static_cast<const uint16_t*>(g)[i]);
@@ -150,9 +177,10 @@ __global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row
                                                                        int64_t nchunks,
                                                                        const float* __restrict__ factor, AdamK k) {
     const int lane = threadIdx.x & (kWave - 1);
-    const int64_t c = chunk_of_block(blockIdx.x, gridDim.x) * kAdamWaves +
-                      __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    if (c >= nchunks) return;
+    // last chunk first: the end of the gradient is what the norm pass read last (still in the MALL)
+    const int64_t c = nchunks - 1 - (chunk_of_block(blockIdx.x, gridDim.x) * kAdamWaves +
+                                     __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
+    if (c < 0) return;
     const float f = factor ? *factor : 1.0f;
     const Row r = rows[chunk_row[c]];
     const int64_t base = (c - r.chunk0) * kChunk;
@@ -236,35 +264,44 @@ __device__ __forceinline__ int advance_row(const Row* __restrict__ rows, int nro
     return lo;
 }
 
+// Exact squares of chunk c (row r) added to acc; KEEP selects ordinary loads instead of nontemporal ones.
+static_assert(kGroups == 1, "sumsq_chunk reads one 128-bit group per lane");
+template <int GDT, bool KEEP>
+__device__ __forceinline__ void sumsq_chunk(const Row& r, int64_t c, int lane, double& acc) {
+    const int64_t base = (c - r.chunk0) * kChunk;
+    const int64_t rem = r.n - base;
+    if (rem >= kChunk && (r.vec & kVecG)) {
+        const int64_t i = base + (int64_t)lane * kVec;
+        const f4 x = KEEP ? load_g4_keep<GDT>(r.g, i) : load_g4<GDT>(r.g, i);
+#pragma unroll
+        for (int e = 0; e < kVec; ++e) acc += sq64(x[e]);
+    } else {
+        const int64_t cnt = rem < kChunk ? rem : kChunk;
+        for (int64_t i = base + lane; i < base + cnt; i += kWave) acc += sq64(load_g1<GDT>(r.g, i));
+    }
+}
+
 // Wave w of the fixed grid takes chunks w, w + W, w + 2W, ... (W = waves in the grid: a workgroup covers 4
 // consecutive chunks = 1024 contiguous elements per step); each lane adds its exact squares in that fixed order.
+// Chunks from keep_from on are read with ordinary loads (two loops, so that the two kinds of load stay apart).
 template <int GDT>
 __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__ rows, int nrows, int64_t nchunks,
-                                                         double* __restrict__ partials) {
+                                                         int64_t keep_from, double* __restrict__ partials) {
     __shared__ double lds[kThreads / kWave];
     const int lane = threadIdx.x & (kWave - 1);
     const int64_t nw = (int64_t)gridDim.x * (kThreads / kWave);
     const int64_t w0 = (int64_t)blockIdx.x * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+    const int64_t split = keep_from < nchunks ? keep_from : nchunks;
     double acc = 0.0;
     int t = 0;
-    for (int64_t c = w0; c < nchunks; c += nw) {
+    int64_t c = w0;
+    for (; c < split; c += nw) {
         t = advance_row(rows, nrows, t, c);
-        const Row r = rows[t];
-        const int64_t base = (c - r.chunk0) * kChunk;
-        const int64_t rem = r.n - base;
-        if (rem >= kChunk && (r.vec & kVecG)) {
-            f4 x[kGroups];
-#pragma unroll
-            for (int u = 0; u < kGroups; ++u) x[u] = load_g4<GDT>(r.g, base + (int64_t)(u * kWave + lane) * kVec);
-#pragma unroll
-            for (int u = 0; u < kGroups; ++u) {
-#pragma unroll
-                for (int e = 0; e < kVec; ++e) acc += sq64(x[u][e]);
-            }
-        } else {
-            const int64_t cnt = rem < kChunk ? rem : kChunk;
-            for (int64_t i = base + lane; i < base + cnt; i += kWave) acc += sq64(load_g1<GDT>(r.g, i));
-        }
+        sumsq_chunk<GDT, false>(rows[t], c, lane, acc);
+    }
+    for (; c < nchunks; c += nw) {
+        t = advance_row(rows, nrows, t, c);
+        sumsq_chunk<GDT, true>(rows[t], c, lane, acc);
     }
     const double s = block_sum(acc, lds);
     if (threadIdx.x == 0) partials[blockIdx.x] = s;
@@ -354,10 +391,11 @@ struct Srcs {
 // partials are then reduced in a fixed order by reduce_partials_kernel).
 constexpr int64_t kSumChunk = (int64_t)kWave * 8;
 
-template <int W>
+template <int W, bool KEEP>
 __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, float scale, uint16_t* out,
-                                                          float* out_sum, double* wave_partials, int vec) {
-    const int64_t c = chunk_of_block(blockIdx.x, gridDim.x);
+                                                          float* out_sum, double* wave_partials, int vec,
+                                                          int64_t chunk_base) {
+    const int64_t c = chunk_base + chunk_of_block(blockIdx.x, gridDim.x);
     const int64_t e0 = c * kSumChunk + (int64_t)threadIdx.x * 8;
     double acc2 = 0.0;
     if (vec && e0 + 8 <= n) {
@@ -379,7 +417,8 @@ __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, flo
         u4 o;
 #pragma unroll
         for (int w = 0; w < 4; ++w) o[w] = pack_bf16(a[2 * w] * scale, a[2 * w + 1] * scale);
-        st(reinterpret_cast<u4*>(out) + gi, o);
+        if (KEEP) st_keep(reinterpret_cast<u4*>(out) + gi, o);
+        else st(reinterpret_cast<u4*>(out) + gi, o);
         if (out_sum) {
             st(reinterpret_cast<f4*>(out_sum) + 2 * gi, f4{a[0], a[1], a[2], a[3]});
             st(reinterpret_cast<f4*>(out_sum) + 2 * gi + 1, f4{a[4], a[5], a[6], a[7]});
@@ -424,14 +463,22 @@ __global__ __launch_bounds__(kThreads) void reduce_partials_kernel(const double*
     if (threadIdx.x == 0) out[blockIdx.x] = t;
 }
 
+// Chunks [0, keep_from) with nontemporal stores of the average, then chunks [keep_from, nchunks) -- the end of the
+// average, which the Adam pass reads first -- with ordinary stores that leave it in the MALL.  Two launches: in one
+// kernel the compiler merges the two kinds of store into one ordinary store.
 template <int W>
-void launch_owner_sum(int world, dim3 grid, hipStream_t st, const Srcs& s, int64_t n, float scale, uint16_t* out,
-                      float* out_sum, double* wave_partials, int vec) {
-    if (world == W)
-        hipLaunchKernelGGL(owner_sum_kernel<W>, grid, dim3(kWave), 0, st, s, n, scale, out, out_sum, wave_partials,
-                           vec);
-    else if constexpr (W > 1)
-        launch_owner_sum<W - 1>(world, grid, st, s, n, scale, out, out_sum, wave_partials, vec);
+void launch_owner_sum(int world, int64_t nchunks, int64_t keep_from, hipStream_t st, const Srcs& s, int64_t n,
+                      float scale, uint16_t* out, float* out_sum, double* wave_partials, int vec) {
+    if (world == W) {
+        if (keep_from > 0)
+            hipLaunchKernelGGL((owner_sum_kernel<W, false>), dim3((unsigned)keep_from), dim3(kWave), 0, st, s, n,
+                               scale, out, out_sum, wave_partials, vec, (int64_t)0);
+        if (nchunks > keep_from)
+            hipLaunchKernelGGL((owner_sum_kernel<W, true>), dim3((unsigned)(nchunks - keep_from)), dim3(kWave), 0,
+                               st, s, n, scale, out, out_sum, wave_partials, vec, keep_from);
+    } else if constexpr (W > 1) {
+        launch_owner_sum<W - 1>(world, nchunks, keep_from, st, s, n, scale, out, out_sum, wave_partials, vec);
+    }
 }
 
 // ------------------------------------------------------------------------------------- scale / cast passes
@@ -650,12 +697,15 @@ int z1_grad_sumsq(const z1_table* table, double* partials, void* stream) {
     int rc = check_table_device(table, &dev);
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t chunk_bytes = kChunk * (table->g_dtype == Z1_F32 ? 4 : 2);
+    const int64_t keep = kMallKeepBytes / chunk_bytes;
+    const int64_t keep_from = table->nchunks > keep ? table->nchunks - keep : 0;
     if (table->g_dtype == Z1_F32)
         hipLaunchKernelGGL(sumsq_kernel<Z1_F32>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows, table->nchunks, partials);
+                           table->nrows, table->nchunks, keep_from, partials);
     else
         hipLaunchKernelGGL(sumsq_kernel<Z1_BF16>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows, table->nchunks, partials);
+                           table->nrows, table->nchunks, keep_from, partials);
     return launch_status();
 }
 
@@ -741,7 +791,9 @@ int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, floa
     hipStream_t st = static_cast<hipStream_t>(stream);
     double* wave_partials = sumsq_partials ? sumsq_partials + Z1_NORM_PARTIALS : nullptr;
     if (nchunks > 0) {
-        launch_owner_sum<Z1_MAX_WORLD>(world, dim3((unsigned)nchunks), st, srcs, n, scale, out_avg, out_sum,
+        const int64_t keep = kMallKeepBytes / (kSumChunk * (int64_t)sizeof(uint16_t));
+        const int64_t keep_from = nchunks > keep ? nchunks - keep : 0;
+        launch_owner_sum<Z1_MAX_WORLD>(world, nchunks, keep_from, st, srcs, n, scale, out_avg, out_sum,
                                        wave_partials, vec);
         const int rc = launch_status();
         if (rc) return rc;
