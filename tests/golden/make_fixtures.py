@@ -4,9 +4,13 @@
 
 Each fixture is an .npz (no pickles) holding the inputs of a small update and the CPU oracle's outputs:
 owner-sum average (c3), the norm n_r, grad_norm, the clipped factor, and the Adam outputs p, m, v, p16 computed
-with that factor.  They are produced by this build's oracle (oracle/z1_oracle.c), not by the reference: the
-reference ships no vectors for this path.
+with that factor.  c1_full_digest.json holds, for the full C1 update (9,438,208 parameters, seed 0, step 1), the
+bits of the norm / grad_norm / factor and the sha256 of the oracle's p, m, v and BF16 outputs, so that a GPU run
+can be checked bit for bit at that size without the oracle.  All are produced by this build's oracle
+(oracle/z1_oracle.c), not by the reference: the reference ships no vectors for this path.
 """
+import hashlib
+import json
 import os
 import sys
 
@@ -67,7 +71,36 @@ def make(name, shapes, seed, kind='normal', step=1, owner=False):
     return out
 
 
+def f32_hex(x):
+    return '0x%08x' % int(np.float32(x).view(np.uint32))
+
+
+def sha256(a):
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def c1_full_digest():
+    """The full C1 update through the oracle: inputs from the package's seeded generator (configs.host_inputs,
+    the one the GPU tests use), clip at 1.0, Adam mode 1 at step 1."""
+    import __graft_entry__
+    __graft_entry__.package()
+    from faster_yoco_amd import configs
+    shapes = configs.C1_SHAPES
+    n = sum(int(np.prod(s)) for s in shapes)
+    x = configs.host_inputs(n, 'c1', seed=0)
+    step = configs.CONFIGS['c1']['step']
+    nr, gn, fac = oracle.norm_clip(oracle.sumsq(x['g']), 1.0, MAX_NORM)
+    po, mo, vo, p16 = oracle.adam_cast(x['g'], x['p'], x['m'], x['v'], step=step, mode=1, factor=fac, **HP)
+    return {'config': 'c1', 'seed': 0, 'shapes': [list(s) for s in shapes], 'params': n, 'step': step, 'mode': 1,
+            'hparams': HP, 'max_norm': MAX_NORM,
+            'norm_bits': f32_hex(nr), 'grad_norm_bits': f32_hex(gn), 'factor_bits': f32_hex(fac),
+            'sha256': {'p': sha256(po), 'm': sha256(mo), 'v': sha256(vo), 'p16': sha256(p16)}}
+
+
 def main():
+    with open(os.path.join(HERE, 'c1_full_digest.json'), 'w') as f:
+        json.dump(c1_full_digest(), f, indent=1)
+        f.write('\n')
     make('c1_mini', MINI, seed=1, step=1)
     make('c2_mini', MINI, seed=2, step=1000)
     make('c3_mini', [(2048,), (3, 333), (64,)], seed=3, step=1000, owner=True)

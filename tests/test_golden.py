@@ -94,3 +94,59 @@ def test_gpu_reproduces_fixture(pkg, dev, path):
     for t, ref in ((p, f['p_out']), (m, f['m_out']), (v, f['v_out'])):
         assert np.array_equal(t.cpu().numpy().view(np.uint32), ref.view(np.uint32))
     assert np.array_equal(configs.bf16_bits(p16), f['p16_out'])
+
+
+def _digest_module():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location('make_fixtures', os.path.join(HERE, 'make_fixtures.py'))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def _committed_digest():
+    import json
+    with open(os.path.join(HERE, 'c1_full_digest.json')) as f:
+        return json.load(f)
+
+
+def test_oracle_reproduces_c1_full_digest(pkg):
+    """The full C1 update (9,438,208 params) through the oracle still gives the committed digests."""
+    assert _digest_module().c1_full_digest() == _committed_digest()
+
+
+@pytest.mark.gpu
+def test_gpu_c1_full_update_matches_digest(pkg, dev):
+    """The full C1 update through the fairseq-shaped optimizer on the GPU: norm, grad_norm and clip factor bits,
+    and the sha256 of p, m, v and the BF16 copy, equal to the oracle's committed digest."""
+    import hashlib
+    from faster_yoco_amd import configs, shard as shard_mod
+    d = _committed_digest()
+    shapes = [tuple(s) for s in d['shapes']]
+    assert shapes == [tuple(s) for s in configs.C1_SHAPES]
+    x = configs.host_inputs(d['params'], 'c1', seed=d['seed'])
+    sh = shard_mod.FlatShard(shapes, dev)
+    start = 0
+    for off, n in zip(sh.offsets, sh.numels):
+        for name in ('g', 'p', 'm', 'v'):
+            getattr(sh, name)[off:off + n].copy_(torch.from_numpy(x[name][start:start + n]))
+        start += n
+    h = d['hparams']
+    opt = shard_mod.Zero1ShardOptimizer(sh, lr=h['lr'], betas=(h['beta1'], h['beta2']), eps=h['eps'],
+                                        weight_decay=h['weight_decay'])
+    opt.step_count = d['step'] - 1
+    gn = opt.clip_grad_norm(d['max_norm'])
+    fac = opt._multiply_factor.clone()
+    opt.step()
+    torch.cuda.synchronize()
+    hexbits = lambda t: '0x%08x' % int(t.reshape(-1)[0].view(torch.int32).item() & 0xffffffff)
+    assert hexbits(opt._norm) == d['norm_bits']
+    assert hexbits(gn) == d['grad_norm_bits']
+    assert hexbits(fac) == d['factor_bits']
+
+    def flat(t):
+        return torch.cat([t[o:o + n] for o, n in zip(sh.offsets, sh.numels)]).cpu().numpy()
+
+    got = {k: hashlib.sha256(flat(getattr(sh, k)).tobytes()).hexdigest() for k in ('p', 'm', 'v')}
+    got['p16'] = hashlib.sha256(flat(sh.p16.view(torch.int16)).tobytes()).hexdigest()
+    assert got == d['sha256']
