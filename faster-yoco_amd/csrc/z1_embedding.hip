@@ -9,8 +9,9 @@
 //
 //   1. keys[i] = id_i (or V when out of range), vals[i] = i;  2. stable radix sort (hipCUB / rocPRIM);
 //   3. row_lo[t] = start of id t's run in the sorted keys (one binary search per t, all in parallel);
-//   4. one wave per output row t writes the row's sums -- or zeros -- exactly once, 8 bf16 columns per lane (aten
-//      zero-fills the whole table and then scatters into it; here every row of the table is written once).
+//   4. one wave per output row t writes the row's sums -- or zeros -- exactly once, 8 bf16 columns per lane, with
+//      nontemporal stores (aten zero-fills the whole table and then scatters into it; here every row of the table
+//      is written once).  Measured: 4 rows per 256-thread workgroup instead of one wave per row, no difference.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
@@ -107,7 +108,8 @@ __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* _
                     o[k >> 1] = (uint32_t)a | ((uint32_t)b << 16);
                 }
             }
-            reinterpret_cast<u4*>(orow)[gi] = o;
+            // nontemporal: the 616 MB table is written once and not read back here (0.155 vs 0.184 ms per call)
+            __builtin_nontemporal_store(o, (__attribute__((address_space(1))) u4*)(reinterpret_cast<u4*>(orow) + gi));
         }
         return;
     }
