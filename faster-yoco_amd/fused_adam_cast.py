@@ -4,7 +4,7 @@ BF16 -> FP32 gradient scale, on gfx950 kernels.
 ``FusedAdamCast`` keeps the reference's interface (``fused_adam_cast.py:48-72``): constructed with ``dest`` (data_ptr
 of an fp32 master -> its BF16 view), called with amp_C.multi_tensor_adam's signature by fairseq's
 FusedAdamV2.step, recording in ``.cast`` the masters whose BF16 copy it wrote.  Differences, all internal:
-  * one persistent-grid launch covers every tensor of the call (tables cached by address), instead of one
+  * one multi-tensor launch covers every tensor of the call (tables cached by address), instead of one
     Triton launch per tensor;
   * ``fold`` / ``fold_factor`` (set by zero1_fast.step) let it read a master's BF16 gradient times the factor
     directly, instead of the FP32 gradient a separate scale pass would have written: the same products

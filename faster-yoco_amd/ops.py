@@ -178,7 +178,7 @@ def bias_corrections(beta1, beta2, step, bias_correction=1):
 
 
 def adam_cast(table, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode):
-    """One persistent-grid Adam + BF16 launch over the table.  factor: 1-element fp32 device tensor or None."""
+    """One multi-tensor Adam + BF16 launch over the table.  factor: 1-element fp32 device tensor or None."""
     with torch.cuda.device(table.device):
         check(lib().z1_adam_cast(table.handle, _scalar(factor, 'adam_cast'), f32(lr), f32(beta1), f32(beta2),
                                  f32(eps), f32(bc1), f32(bc2), f32(weight_decay), int(mode),

@@ -6,9 +6,12 @@ The same switches select it (read at import, off by default, yoco/tasks/zero1_fa
     YOCO_Z1_ONE_PASS, YOCO_Z1_SCALE_KERNEL, YOCO_FUSED_ADAM, YOCO_CE_ALLGATHER
 plus one of this build, YOCO_Z1_FOLD_SCALE (default 1): with the fused Adam installed, the Adam kernel reads each
 owned BF16 gradient times the factor itself instead of a scale pass writing the FP32 gradient first (identical
-products).  ``install(mixin)`` swaps ``clip_grad_norm`` / ``step`` / ``zero_grad`` on fairseq's
-``_FP16OptimizerMixin`` (or any class with its attributes) exactly where the reference does (:252-255);
-``install_fairseq()`` does it on the real fairseq when importable.
+products).  The FP32 masters' ``.grad`` tensors are then not written by the step; set YOCO_Z1_FOLD_SCALE=0 where
+something reads them afterwards.
+
+``install(mixin)`` swaps ``clip_grad_norm`` / ``step`` / ``zero_grad`` on fairseq's ``_FP16OptimizerMixin`` (or any
+class with its attributes) exactly where the reference does (:252-255); ``install_fairseq()`` does it on the real
+fairseq when importable.
 
 The same surface as the reference: ``clip_grad_norm(self, max_norm, aggregate_norm_fn=None) -> Tensor`` (0-d fp32,
 on device, no host sync), ``step(self, closure=None, groups=None)``, ``zero_grad(self)``.  The norm is this

@@ -112,7 +112,7 @@ int z1_update_scalars_run(const double* partials, const z1_update_scalars* u, vo
 int z1_clip_factor(const float* norm, const float* factor_in, float factor_value, float* grad_norm_out,
                    float* factor_out, float max_norm, void* stream);
 
-/* Fused Adam + BF16 copy over every row of the table in one persistent-grid launch (replaces the per-tensor
+/* Fused Adam + BF16 copy over every row of the table in one multi-tensor launch (replaces the per-tensor
  * Triton _adam launches of yoco/tasks/fused_adam_cast.py:19-45,62-72, and folds the gradient factor multiply of
  * yoco/tasks/zero1_fast.py:175-192 / scale_up :75-89 into the gradient load).  factor: device fp32 scalar or NULL
  * (1.0).  lr .. weight_decay are the fp32 kernel scalars; bc1, bc2 as fused_adam_cast.py:58-60 rounds them. */

@@ -1,0 +1,93 @@
+"""The shard update captured in a HIP graph (torch.cuda.graph): norm + clip + Adam + BF16 copy, and the owner-sum
+form (owner sum with the fused norm, clip, Adam), each replayed several times from a restored state -- with eager
+work and synchronisations between the replays -- and every replay bit-identical to the same update run eagerly.
+
+The update launches only kernels on the current stream (the tables and the norm workspace are made at set-up, and
+nothing in it clears memory with a memset), so it can be captured once per step and replayed; the bias corrections
+are kernel arguments rounded on the host, so a graph holds one step's."""
+import numpy as np
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+HP = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+
+
+def make(dev, shapes, grad_dtype, seed, step):
+    from faster_yoco_amd import shard as shard_mod
+    sh = shard_mod.FlatShard(shapes, dev, grad_dtype=grad_dtype)
+    rng = np.random.default_rng(seed)
+    n = sh.total
+    sh.p.copy_(torch.from_numpy((rng.standard_normal(n) * 0.02).astype(np.float32)))
+    sh.m.copy_(torch.from_numpy((rng.standard_normal(n) * 1e-4).astype(np.float32)))
+    sh.v.copy_(torch.from_numpy(np.abs(rng.standard_normal(n) * 1e-8).astype(np.float32)))
+    g = torch.from_numpy((rng.standard_normal(n) * 3e-3).astype(np.float32))
+    sh.g.copy_(g.to(grad_dtype))
+    opt = shard_mod.Zero1ShardOptimizer(sh, **HP)
+    opt.step_count = step - 1
+    return sh, opt
+
+
+def snapshot(sh):
+    return {k: getattr(sh, k).clone() for k in ('g', 'p', 'm', 'v', 'p16')}
+
+
+def restore(sh, snap):
+    for k, t in snap.items():
+        getattr(sh, k).copy_(t)
+
+
+def bits(t):
+    return t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32)
+
+
+def check_same(sh, ref):
+    for k in ('p', 'm', 'v', 'p16'):
+        assert torch.equal(bits(getattr(sh, k)), bits(ref[k])), k
+
+
+def contributions(n, dev, seed):
+    rng = np.random.default_rng(seed)
+    return [torch.from_numpy((rng.standard_normal(n) * 1e-3).astype(np.float32)).to(dev).to(torch.bfloat16)
+            for _ in range(8)]
+
+
+@pytest.mark.parametrize('form', ['norm', 'owner_sum'])
+def test_update_graph_replays_match_eager(pkg, dev, form):
+    from faster_yoco_amd import configs
+    step = 7
+    gdt = torch.bfloat16 if form == 'owner_sum' else torch.float32
+    sh, opt = make(dev, configs.C1_SHAPES, gdt, seed=11, step=step)
+    contribs = contributions(sh.total, dev, 12) if form == 'owner_sum' else None
+    snap = snapshot(sh)
+
+    def update():
+        if contribs is not None:
+            opt.reduce_grads(contribs)
+        return opt.update(1.0)
+
+    # eager reference of this step
+    gn_eager = update().clone()
+    torch.cuda.synchronize()
+    ref = snapshot(sh)
+
+    # capture the same step (nothing runs during capture), then replay from the restored state
+    restore(sh, snap)
+    opt.step_count = step - 1
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):                  # captures on torch's capture stream, the current one inside
+        gn_graph = update()
+    torch.cuda.synchronize()
+    assert opt.step_count == step
+    for rep in range(3):
+        restore(sh, snap)
+        junk = torch.randn(1 << 20, device=dev).sum()          # eager work between the replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(gn_graph.reshape(1)), bits(gn_eager.reshape(1))), rep
+        check_same(sh, ref)
+        del junk
+    graph.reset()
