@@ -15,9 +15,10 @@
  * written, division and square root are the IEEE correctly rounded SSE instructions, subnormals are kept.
  *
  * Pins (checked in tests/test_oracle_pins.py): torch CPU's float->bfloat16 conversion, torch CPU fp32 adds in rank
- * order, torch's own tensor/scalar expressions for the clip chain, torch.optim.AdamW within a few ulp, closed-form
- * special cases (lr=0, g=0 pure decay, wd=0 mode equality, step-1 sign update) and an exact-rational restatement
- * with a single rounding per operation.
+ * order, torch's own tensor/scalar expressions for the clip chain and the trainer's scalar chain, torch.optim.AdamW
+ * within a few ulp, closed-form special cases (lr=0, g=0 pure decay, wd=0 mode equality, step-1 sign update), an
+ * exact-rational restatement with a single rounding per operation, and for the embedding gradient exact cases plus
+ * one only aten's runs-of-10 partial sums get right.
  */
 #include <math.h>
 #include <stdint.h>
