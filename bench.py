@@ -136,6 +136,51 @@ def glue_timing(opt, hp, iters=200):
     return out
 
 
+def dropin_timing(dev, hp, step, reps=10):
+    """The drop-in surface at C2's size: FusedAdamCast called with amp_C.multi_tensor_adam's signature (as
+    fairseq's FusedAdamV2.step calls it) over the 38 C2 tensors allocated one by one (the reference's
+    per-parameter layout, BF16 destinations as views of one flat buffer), once with fp32 gradients and once with
+    the BF16 gradients folded in (zero1_fast's default); HIP events on the current stream, ms per call."""
+    import torch
+    from faster_yoco_amd import configs
+    from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+    shapes = configs.shapes('c2')
+    numels = [math.prod(s) for s in shapes]
+    flat16 = torch.empty(sum(numels), dtype=torch.bfloat16, device=dev)
+    gs, ps, ms, vs, g16s, dest, off = [], [], [], [], [], {}, 0
+    for s, n in zip(shapes, numels):
+        p = torch.empty(s, device=dev).normal_(0.0, 0.02)
+        gs.append(torch.empty(s, device=dev).normal_(0.0, 1e-4))
+        ms.append(torch.empty(s, device=dev).normal_(0.0, 1e-4))
+        vs.append(torch.empty(s, device=dev).normal_(0.0, 1e-8).abs_())
+        g16s.append(gs[-1].to(torch.bfloat16))
+        ps.append(p)
+        dest[p.data_ptr()] = flat16[off:off + n].view(s)
+        off += n
+    fa = FusedAdamCast(dest)
+    noop = torch.zeros(1, dtype=torch.int32, device=dev)
+    factor = torch.full((1,), 0.5, dtype=torch.float32, device=dev)
+    out = {'tensors': len(shapes), 'params': sum(numels)}
+    for name, fold in (('fp32_grads_ms', False), ('folded_bf16_grads_ms', True)):
+        if fold:
+            fa.fold, fa.fold_factor = {p.data_ptr(): g for p, g in zip(ps, g16s)}, factor
+        call = lambda: fa(2048 * 32, noop, [gs, ps, ms, vs], hp['lr'], hp['betas'][0], hp['betas'][1], hp['eps'],
+                          step, 1, 1, hp['weight_decay'])
+        for _ in range(3):
+            call()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(e0.elapsed_time(e1) / reps, 4)
+        fa.cast.clear()
+    fa.fold, fa.fold_factor = {}, None
+    return out
+
+
 def embedding_timing(dev, reps=20):
     """The embedding owner's gradient at the recipe's size (8 ranks x 2048 token rows of 3072, vocabulary 100,288):
     torch's aten.embedding_dense_backward + x 1/world as the reference runs it, against this build's fused kernel;
@@ -277,6 +322,8 @@ def main():
         'trainer_scalar_chain_us': glue_timing(opt, hp),
         'owner_embedding_grad_ms': embedding_timing(dev),
     }
+    if cfg == 'c2':
+        out['dropin_multi_tensor_adam'] = dropin_timing(dev, hp, step0)
     print(json.dumps(out), flush=True)
 
 
