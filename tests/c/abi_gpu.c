@@ -1,0 +1,222 @@
+/* Plain-C, torch-free consumer of include/yoco_z1.h on the GPU (what a binding from another language does):
+ * device buffers from hipMalloc, every call through the C ABI on the null stream, results checked against the CPU
+ * oracle's C functions (oracle/z1_oracle.c, test infrastructure) at the parity bars of the Python suite:
+ *   1. a 4-row table (tails, a row below one chunk, 64-element row alignment): sum of squares -> norm + clip
+ *      -> Adam + BF16 copy with the device factor; norm within 1e-6 of the exact one, the clip chain bit-exact
+ *      from the GPU's norm, p / m / v / BF16 bit-exact given the GPU's factor;
+ *   2. the owner sum of 8 BF16 contributions with the fused norm: average and FP32 sum bit-exact, norm within
+ *      1e-6 of the average's exact norm.
+ * Built by __graft_entry__.build() with gcc, linked against libyoco_z1.so, the oracle and the HIP runtime, twice:
+ * as tests/c/libabi_gpu.so, whose abi_gpu_run() tests/test_gpu_c_abi.py calls in-process, and with -DABI_GPU_MAIN
+ * as the standalone program tests/c/abi_gpu.  Returns (exits with) 0 and prints "ok" on success. */
+#include <hip/hip_runtime_api.h>
+
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "yoco_z1.h"
+
+/* oracle/z1_oracle.c */
+uint16_t oracle_bf16_rne(float x);
+void oracle_owner_sum(const uint16_t* const* src, int world, int64_t n, float scale, uint16_t* out, float* out_sum);
+double oracle_sumsq_f32(const float* g, int64_t n);
+double oracle_sumsq_bf16(const uint16_t* g, int64_t n);
+void oracle_norm_clip(double sumsq, float factor, float max_norm, float* out);
+void oracle_bias_corrections(double beta1, double beta2, int64_t step, int bias_correction, float* out);
+void oracle_adam_cast(const void* g, int g_bf16, float* p, float* m, float* v, uint16_t* p16, int64_t n,
+                      float factor, int apply_factor, float lr, float beta1, float beta2, float eps, float bc1,
+                      float bc2, float wd, int mode);
+
+#define HIP_OK(x)                                                                                   \
+    do {                                                                                            \
+        hipError_t e_ = (x);                                                                        \
+        if (e_ != hipSuccess) {                                                                     \
+            fprintf(stderr, "%s:%d: %s\n", __FILE__, __LINE__, hipGetErrorString(e_));              \
+            return 2;                                                                               \
+        }                                                                                           \
+    } while (0)
+#define Z1_OK_(x)                                                                                   \
+    do {                                                                                            \
+        int r_ = (x);                                                                               \
+        if (r_ != Z1_OK) {                                                                          \
+            fprintf(stderr, "%s:%d: %s\n", __FILE__, __LINE__, z1_strerror(r_));                    \
+            return 3;                                                                               \
+        }                                                                                           \
+    } while (0)
+#define EXPECT(c)                                                                                   \
+    do {                                                                                            \
+        if (!(c)) {                                                                                 \
+            fprintf(stderr, "%s:%d: check failed: %s\n", __FILE__, __LINE__, #c);                   \
+            return 4;                                                                               \
+        }                                                                                           \
+    } while (0)
+
+static uint64_t rng = 0x9E3779B97F4A7C15ull;
+
+static double unif(void) {                       /* xorshift64*, 53-bit uniform in (0, 1) */
+    rng ^= rng >> 12;
+    rng ^= rng << 25;
+    rng ^= rng >> 27;
+    return ((double)((rng * 0x2545F4914F6CDD1Dull) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
+}
+
+static float normal(double sd) {                 /* Box-Muller */
+    return (float)(sd * sqrt(-2.0 * log(unif())) * cos(6.283185307179586 * unif()));
+}
+
+static uint32_t bits(float x) {
+    uint32_t u;
+    memcpy(&u, &x, 4);
+    return u;
+}
+
+static int same_f32(const float* a, const float* b, int64_t n) { return memcmp(a, b, (size_t)n * 4) == 0; }
+
+static int table_update(void) {
+    enum { R = 4 };
+    const int64_t sizes[R] = {70001, 256 * 37, 100, 4096 * 3 + 7};
+    int64_t off[R], total = 0;
+    for (int i = 0; i < R; ++i) {
+        off[i] = total;
+        total += (sizes[i] + 63) / 64 * 64;
+    }
+    float *hg = malloc(total * 4), *hp = malloc(total * 4), *hm = malloc(total * 4), *hv = malloc(total * 4);
+    float *op = malloc(total * 4), *om = malloc(total * 4), *ov = malloc(total * 4);
+    uint16_t *h16 = malloc(total * 2), *o16 = malloc(total * 2);
+    for (int64_t i = 0; i < total; ++i) {
+        hg[i] = normal(1e-2);                    /* norm about 3.1 over these ~95K elements: the clip is active */
+        hp[i] = normal(0.02);
+        hm[i] = normal(1e-4);
+        hv[i] = fabsf(normal(1e-8));
+    }
+    float *dg, *dp, *dm, *dv, *ds;
+    uint16_t* d16;
+    double* dpart;
+    HIP_OK(hipMalloc((void**)&dg, total * 4));
+    HIP_OK(hipMalloc((void**)&dp, total * 4));
+    HIP_OK(hipMalloc((void**)&dm, total * 4));
+    HIP_OK(hipMalloc((void**)&dv, total * 4));
+    HIP_OK(hipMalloc((void**)&d16, total * 2));
+    HIP_OK(hipMalloc((void**)&ds, 3 * 4));
+    HIP_OK(hipMalloc((void**)&dpart, Z1_NORM_PARTIALS * 8));
+    HIP_OK(hipMemcpy(dg, hg, total * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dp, hp, total * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dm, hm, total * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dv, hv, total * 4, hipMemcpyHostToDevice));
+
+    z1_tensor rows[R];
+    for (int i = 0; i < R; ++i) {
+        rows[i].g = dg + off[i];
+        rows[i].p = dp + off[i];
+        rows[i].m = dm + off[i];
+        rows[i].v = dv + off[i];
+        rows[i].p16 = d16 + off[i];
+        rows[i].n = sizes[i];
+    }
+    z1_table* t = NULL;
+    Z1_OK_(z1_table_create(rows, R, Z1_F32, &t));
+    int64_t numel = 0, nch = 0;
+    int nr = 0;
+    Z1_OK_(z1_table_info(t, &numel, &nch, &nr));
+    EXPECT(nr == R && numel == sizes[0] + sizes[1] + sizes[2] + sizes[3]);
+
+    const float lr = 3e-4f, b1 = 0.9f, b2 = 0.95f, eps = 1e-8f, wd = 0.1f, max_norm = 1.0f;
+    const int64_t step = 1000;
+    float bc[2];
+    oracle_bias_corrections(0.9, 0.95, step, 1, bc);
+    Z1_OK_(z1_grad_sumsq(t, dpart, NULL));
+    Z1_OK_(z1_norm_clip(dpart, NULL, 1.0f, ds + 0, ds + 1, ds + 2, max_norm, NULL));
+    Z1_OK_(z1_adam_cast(t, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL));
+    HIP_OK(hipDeviceSynchronize());
+    float sc[3];
+    HIP_OK(hipMemcpy(sc, ds, 12, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(op, dp, total * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(om, dm, total * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(ov, dv, total * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(o16, d16, total * 2, hipMemcpyDeviceToHost));
+
+    double ss = 0.0;
+    for (int i = 0; i < R; ++i) ss += oracle_sumsq_f32(hg + off[i], sizes[i]);
+    const double exact = sqrt(ss);
+    EXPECT(fabs((double)sc[0] - exact) <= 1e-6 * exact);
+    float chain[3];
+    oracle_norm_clip((double)sc[0] * (double)sc[0], 1.0f, max_norm, chain);    /* entered at the GPU's norm */
+    EXPECT(bits(chain[0]) == bits(sc[0]) && bits(chain[1]) == bits(sc[1]) && bits(chain[2]) == bits(sc[2]));
+    EXPECT(sc[2] < 1.0f);                                                      /* the clip is active */
+    for (int i = 0; i < R; ++i) {
+        const int64_t o = off[i], n = sizes[i];
+        oracle_adam_cast(hg + o, 0, hp + o, hm + o, hv + o, h16 + o, n, sc[2], 1, lr, b1, b2, eps, bc[0], bc[1], wd,
+                         1);
+        EXPECT(same_f32(op + o, hp + o, n) && same_f32(om + o, hm + o, n) && same_f32(ov + o, hv + o, n));
+        EXPECT(memcmp(o16 + o, h16 + o, (size_t)n * 2) == 0);
+    }
+    Z1_OK_(z1_table_destroy(t));
+    HIP_OK(hipFree(dg));
+    HIP_OK(hipFree(dp));
+    HIP_OK(hipFree(dm));
+    HIP_OK(hipFree(dv));
+    HIP_OK(hipFree(d16));
+    HIP_OK(hipFree(ds));
+    HIP_OK(hipFree(dpart));
+    free(hg); free(hp); free(hm); free(hv); free(op); free(om); free(ov); free(h16); free(o16);
+    return 0;
+}
+
+static int owner_sum(void) {
+    enum { W = 8 };
+    const int64_t n = 100003;                    /* odd: a vector body and an element-wise tail */
+    uint16_t* hc[W];
+    uint16_t* dc[W];
+    for (int k = 0; k < W; ++k) {
+        hc[k] = malloc(n * 2);
+        for (int64_t i = 0; i < n; ++i) hc[k][i] = oracle_bf16_rne(normal(1e-3));
+        HIP_OK(hipMalloc((void**)&dc[k], n * 2));
+        HIP_OK(hipMemcpy(dc[k], hc[k], n * 2, hipMemcpyHostToDevice));
+    }
+    const int64_t nws = z1_owner_sum_workspace(n);
+    EXPECT(nws >= Z1_NORM_PARTIALS);
+    uint16_t *davg, *havg = malloc(n * 2), *eavg = malloc(n * 2);
+    float *dsum, *hsum = malloc(n * 4), *esum = malloc(n * 4), *dnr;
+    double* dws;
+    HIP_OK(hipMalloc((void**)&davg, n * 2));
+    HIP_OK(hipMalloc((void**)&dsum, n * 4));
+    HIP_OK(hipMalloc((void**)&dws, nws * 8));
+    HIP_OK(hipMalloc((void**)&dnr, 4));
+    Z1_OK_(z1_owner_sum_bf16((const uint16_t* const*)dc, W, n, 0.125f, davg, dsum, dws, NULL));
+    Z1_OK_(z1_norm_clip(dws, NULL, 1.0f, dnr, NULL, NULL, 0.0f, NULL));
+    HIP_OK(hipDeviceSynchronize());
+    float nrm;
+    HIP_OK(hipMemcpy(havg, davg, n * 2, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(hsum, dsum, n * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(&nrm, dnr, 4, hipMemcpyDeviceToHost));
+    oracle_owner_sum((const uint16_t* const*)hc, W, n, 0.125f, eavg, esum);
+    EXPECT(memcmp(havg, eavg, (size_t)n * 2) == 0);
+    EXPECT(same_f32(hsum, esum, n));
+    const double exact = sqrt(oracle_sumsq_bf16(eavg, n));
+    EXPECT(fabs((double)nrm - exact) <= 1e-6 * exact);
+    for (int k = 0; k < W; ++k) {
+        HIP_OK(hipFree(dc[k]));
+        free(hc[k]);
+    }
+    HIP_OK(hipFree(davg));
+    HIP_OK(hipFree(dsum));
+    HIP_OK(hipFree(dws));
+    HIP_OK(hipFree(dnr));
+    free(havg); free(eavg); free(hsum); free(esum);
+    return 0;
+}
+
+int abi_gpu_run(void) {
+    int rc = table_update();
+    if (rc == 0) rc = owner_sum();
+    printf("%s\n", rc ? "FAIL" : "ok");
+    fflush(stdout);
+    return rc;
+}
+
+#ifdef ABI_GPU_MAIN
+int main(void) { return abi_gpu_run(); }
+#endif
