@@ -164,3 +164,100 @@ def to_device_bf16(h, device):
 def bf16_bits(t):
     """bf16 tensor -> uint16 NumPy bits (host copy)."""
     return t.detach().view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+# --------------------------------------------------------------------------------------------- hashed inputs
+# Inputs that NumPy on the host and torch on the device compute bit for bit alike, so that a full-size update can
+# be checked against digests of the CPU oracle's outputs without regenerating the inputs on the host: a 32-bit
+# integer hash of (stream, element index) in 64-bit integer arithmetic whose products stay below 2^63, turned
+# into floats that are small integers times powers of two (exact in fp32; the BF16 contributions exact in bf16).
+_M32 = 0xFFFFFFFF
+_STREAM = {'p': 1, 'm': 2, 'v': 3, 'g': 4, 'scale': 5, 'pick': 6, 'sign': 7}   # contribution r: 16 + r
+HASHED_CONFIGS = ('c2', 'c3', 'c5')
+
+
+def _mix32(x):
+    x = x ^ (x >> 16)
+    x = (x * 0x7FEB352D) & _M32
+    x = x ^ (x >> 15)
+    x = (x * 0x68E31DA5) & _M32
+    return x ^ (x >> 16)
+
+
+def _hash(idx, stream):
+    return _mix32((_mix32(idx) + stream * 0x9E3779B1) & _M32)
+
+
+class _NP:
+    @staticmethod
+    def f32(x):
+        return x.astype(np.float32)
+
+    @staticmethod
+    def pow2(e):                     # 2**-e as float32, exactly, from its bits
+        return ((127 - e) << 23).astype(np.int32).view(np.float32)
+
+    where, abs = staticmethod(np.where), staticmethod(np.abs)
+
+
+class _TORCH:
+    @staticmethod
+    def f32(x):
+        return x.to(torch.float32)
+
+    @staticmethod
+    def pow2(e):
+        return ((127 - e) << 23).to(torch.int32).view(torch.float32)
+
+    where, abs = staticmethod(torch.where), staticmethod(torch.abs)
+
+
+def hashed_values(name, field, idx):
+    """Values of `field` ('p', 'm', 'v', 'g' or 'c0'..'c7', a BF16 contribution given as fp32) of config `name`
+    at the int64 element indices `idx` (a NumPy array or a torch tensor, which decides where it is computed).
+    p ~ U[-2^-5, 2^-5), m, g ~ U[-2^-13, 2^-13), v ~ U[0, 2^-27), 24-bit integers times powers of two; c5's g
+    spreads each value over 24 binades by a hashed power of two and sets about 0.1% to +-1e4; the c3
+    contributions are 8-bit integers times 2^-19 (exact in bf16)."""
+    xp = _NP if isinstance(idx, np.ndarray) else _TORCH
+    if field.startswith('c'):
+        h = _hash(idx, 16 + int(field[1:]))
+        return xp.f32((h >> 24) - 128) * np.float32(2.0 ** -19)
+    s24 = xp.f32((_hash(idx, _STREAM[field]) >> 8) - (1 << 23))
+    if field == 'p':
+        return s24 * np.float32(2.0 ** -28)
+    if field == 'm':
+        return s24 * np.float32(2.0 ** -36)
+    if field == 'v':
+        return xp.abs(s24) * np.float32(2.0 ** -50)
+    if name == 'c5':
+        g = s24 * xp.pow2(29 + _hash(idx, _STREAM['scale']) % 24)
+        big = xp.where((_hash(idx, _STREAM['sign']) & 1) == 1, np.float32(1e4), np.float32(-1e4))
+        return xp.where(_hash(idx, _STREAM['pick']) % 1000 == 0, big, g)
+    return s24 * np.float32(2.0 ** -36)
+
+
+def fill_shard_hashed(shard, name, chunk=1 << 25):
+    """The hashed inputs of config `name` written into a FlatShard on its device (element k of the concatenated
+    tensor list gets index k; alignment gaps are left alone).  p16 = bf16(p).  Returns the eight BF16
+    contributions (flat, laid out like the shard's gradient) for 'c3', else None."""
+    dev = shard.device
+    fields = ['p', 'm', 'v'] + ([] if name == 'c3' else ['g'])
+    contribs = None
+    if name == 'c3':
+        contribs = [torch.zeros(shard.total, dtype=torch.bfloat16, device=dev) for _ in range(8)]
+    k = 0
+    for off, n in zip(shard.offsets, shard.numels):
+        for i in range(0, n, chunk):
+            m = min(chunk, n - i)
+            idx = torch.arange(k + i, k + i + m, dtype=torch.int64, device=dev)
+            for f in fields:
+                getattr(shard, f)[off + i:off + i + m] = hashed_values(name, f, idx).to(getattr(shard, f).dtype)
+            if contribs is not None:
+                for r in range(8):
+                    contribs[r][off + i:off + i + m] = hashed_values(name, f'c{r}', idx).to(torch.bfloat16)
+        k += n
+    if shard.p16 is not None:
+        shard.p16.copy_(shard.p)
+    if name == 'c3':
+        shard.g.zero_()
+    return contribs

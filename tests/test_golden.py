@@ -150,3 +150,23 @@ def test_gpu_c1_full_update_matches_digest(pkg, dev):
     got = {k: hashlib.sha256(flat(getattr(sh, k)).tobytes()).hexdigest() for k in ('p', 'm', 'v')}
     got['p16'] = hashlib.sha256(flat(sh.p16.view(torch.int16)).tobytes()).hexdigest()
     assert got == d['sha256']
+
+
+def test_hashed_inputs_match_large_digest_prefixes(pkg):
+    """The hashed input generator (NumPy and torch on the CPU, bit for bit alike) still gives the input prefixes the
+    large digests were made from."""
+    import hashlib
+    import json
+    from faster_yoco_amd import configs
+    with open(os.path.join(HERE, 'large_digests.json')) as f:
+        digests = json.load(f)
+    for name, d in digests.items():
+        P = d['prefix_elements']
+        idx = np.arange(P, dtype=np.int64)
+        for field, want in d['input_prefix_sha256'].items():
+            a = configs.hashed_values(name, field, idx)
+            b = configs.hashed_values(name, field, torch.from_numpy(idx)).numpy()
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (name, field)
+            if field.startswith('c'):
+                a = (a.view(np.uint32) >> 16).astype(np.uint16)
+            assert hashlib.sha256(a.tobytes()).hexdigest() == want, (name, field)
