@@ -11,7 +11,7 @@ import torch
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_NAME = 'libyoco_z1.so'
-# YOCO_Z1_LIB selects another build of the same library (e.g. one compiled with different tuning macros)
+# YOCO_Z1_LIB selects another build of the same C ABI (e.g. an older build, for an A/B timing of two versions)
 LIB_PATH = os.environ.get('YOCO_Z1_LIB') or os.path.join(_HERE, LIB_NAME)
 
 Z1_F32 = 0

@@ -173,7 +173,7 @@ def bf16_bits(t):
 # into floats that are small integers times powers of two (exact in fp32; the BF16 contributions exact in bf16).
 _M32 = 0xFFFFFFFF
 _STREAM = {'p': 1, 'm': 2, 'v': 3, 'g': 4, 'scale': 5, 'pick': 6, 'sign': 7}   # contribution r: 16 + r
-HASHED_CONFIGS = ('c2', 'c3', 'c5')
+HASHED_CONFIGS = ('c2', 'c3', 'c5', 'c4')
 
 
 def _mix32(x):
@@ -184,7 +184,21 @@ def _mix32(x):
     return x ^ (x >> 16)
 
 
+def _mix32_u32(x):
+    """_mix32 in place on a NumPy uint32 array, whose products wrap modulo 2^32 (the same values, less memory)."""
+    x ^= x >> 16
+    x *= np.uint32(0x7FEB352D)
+    x ^= x >> 15
+    x *= np.uint32(0x68E31DA5)
+    x ^= x >> 16
+    return x
+
+
 def _hash(idx, stream):
+    if isinstance(idx, np.ndarray):
+        x = _mix32_u32(idx.astype(np.uint32))              # element indices are below 2^32
+        x += np.uint32((stream * 0x9E3779B1) & _M32)
+        return _mix32_u32(x).astype(np.int64)
     return _mix32((_mix32(idx) + stream * 0x9E3779B1) & _M32)
 
 

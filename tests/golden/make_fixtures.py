@@ -1,7 +1,7 @@
 """Writes the committed golden fixtures (inputs + oracle outputs) for the parity suite.
 
     python tests/golden/make_fixtures.py            # the small fixtures and the C1 digest (seconds)
-    python tests/golden/make_fixtures.py --large    # large_digests.json: C2, C3, C5 at full size (minutes)
+    python tests/golden/make_fixtures.py --large    # large_digests.json: C2, C3, C5, C4 at full size (minutes)
 
 Each fixture is an .npz (no pickles) holding the inputs of a small update and the CPU oracle's outputs:
 owner-sum average (c3), the norm n_r, grad_norm, the clipped factor, and the Adam outputs p, m, v, p16 computed
@@ -101,53 +101,55 @@ def c1_full_digest():
 PREFIX = 1 << 20                      # elements of each input whose digest is recorded (input check on the GPU)
 
 
-def _hashed_array(configs, name, field, n, chunk=1 << 25):
-    out = np.empty(n, np.float32)
-    for lo in range(0, n, chunk):
-        hi = min(n, lo + chunk)
-        out[lo:hi] = configs.hashed_values(name, field, np.arange(lo, hi, dtype=np.int64))
-    return out
-
-
-def large_digest(name):
-    """The full-size update of config `name` (c2, c3 or c5: the 430,662,912-parameter shard) on the hashed inputs
-    of configs.hashed_values, through the oracle: c3 first sums the eight BF16 contributions in rank order (x 1/8);
-    then norm -> clip at 1.0 -> Adam mode 1 at step 1000 with the clipped factor.  Records the bits of the norm,
-    grad_norm and factor, sha256 of p, m, v, the BF16 copy (and of the BF16 average for c3), and sha256 of the
-    first PREFIX elements of every input.  Takes minutes and ~20 GB of host memory."""
+def large_digest(name, chunk=1 << 25):
+    """The full-size update of config `name` (c2, c3, c5: the 430,662,912-parameter shard; c4: 3,445,303,296) on
+    the hashed inputs of configs.hashed_values, through the oracle, streamed in chunks of `chunk` elements: pass 1
+    sums the squares of the gradient (c3: of the rank-order BF16 average of the eight contributions, x 1/8), the
+    chunk sums added in FP64; norm -> clip at 1.0; pass 2 runs Adam mode 1 at step 1000 with the clipped factor and
+    feeds sha256 of p, m, v, the BF16 copy (and the BF16 average for c3).  Also records the bits of the norm,
+    grad_norm and factor and sha256 of the first PREFIX elements of every input.  Takes minutes."""
     import __graft_entry__
     __graft_entry__.package()
     from faster_yoco_amd import configs
     n = configs.numel(name)
-    x = {f: _hashed_array(configs, name, f, n) for f in ('p', 'm', 'v')}
-    prefix = {f: sha256(x[f][:PREFIX]) for f in ('p', 'm', 'v')}
-    out = {}
-    if name == 'c3':
-        contribs = []
-        for r in range(8):
-            c = _hashed_array(configs, name, f'c{r}', n)
-            contribs.append((c.view(np.uint32) >> 16).astype(np.uint16))
-            del c
-            prefix[f'c{r}'] = sha256(contribs[-1][:PREFIX])
-        g = oracle.owner_sum(contribs)
-        del contribs
-        out['avg16'] = sha256(g)
-    else:
-        g = _hashed_array(configs, name, 'g', n)
-        prefix['g'] = sha256(g[:PREFIX])
     step = configs.CONFIGS[name]['step']
-    nr, gn, fac = oracle.norm_clip(oracle.sumsq(g), 1.0, MAX_NORM)
-    po, mo, vo, p16 = oracle.adam_cast(g, x['p'], x['m'], x['v'], step=step, mode=1, factor=fac, **HP)
-    out.update(p=sha256(po), m=sha256(mo), v=sha256(vo), p16=sha256(p16))
+    gfields = [f'c{r}' for r in range(8)] if name == 'c3' else ['g']
+
+    def values(field, lo, hi, sub=1 << 18):          # pieces small enough for malloc's heap (no page faults)
+        a = np.empty(hi - lo, np.float32)
+        for s in range(lo, hi, sub):
+            e = min(hi, s + sub)
+            a[s - lo:e - lo] = configs.hashed_values(name, field, np.arange(s, e, dtype=np.int64))
+        return (a.view(np.uint32) >> 16).astype(np.uint16) if field.startswith('c') else a
+
+    def grad(lo, hi):
+        if name != 'c3':
+            return values('g', lo, hi)
+        return oracle.owner_sum([values(f, lo, hi) for f in gfields])
+
+    prefix = {f: sha256(values(f, 0, PREFIX)) for f in ['p', 'm', 'v'] + gfields}
+    ss = 0.0
+    for lo in range(0, n, chunk):
+        ss += oracle.sumsq(grad(lo, min(n, lo + chunk)))
+    nr, gn, fac = oracle.norm_clip(ss, 1.0, MAX_NORM)
+    hs = {k: hashlib.sha256() for k in (['avg16'] if name == 'c3' else []) + ['p', 'm', 'v', 'p16']}
+    for lo in range(0, n, chunk):
+        hi = min(n, lo + chunk)
+        g = grad(lo, hi)
+        po, mo, vo, p16 = oracle.adam_cast(g, values('p', lo, hi), values('m', lo, hi), values('v', lo, hi),
+                                           step=step, mode=1, factor=fac, **HP)
+        for k, a in (('avg16', g), ('p', po), ('m', mo), ('v', vo), ('p16', p16)):
+            if k in hs:
+                hs[k].update(np.ascontiguousarray(a).tobytes())
     return {'config': name, 'params': n, 'step': step, 'mode': 1, 'hparams': HP, 'max_norm': MAX_NORM,
             'inputs': 'faster_yoco_amd.configs.hashed_values', 'prefix_elements': PREFIX,
             'norm_bits': f32_hex(nr), 'grad_norm_bits': f32_hex(gn), 'factor_bits': f32_hex(fac),
-            'sha256': out, 'input_prefix_sha256': prefix}
+            'sha256': {k: h.hexdigest() for k, h in hs.items()}, 'input_prefix_sha256': prefix}
 
 
 def main():
     if '--large' in sys.argv[1:]:
-        d = {name: large_digest(name) for name in ('c2', 'c3', 'c5')}
+        d = {name: large_digest(name) for name in ('c2', 'c3', 'c5', 'c4')}
         with open(os.path.join(HERE, 'large_digests.json'), 'w') as f:
             json.dump(d, f, indent=1)
             f.write('\n')
