@@ -13,6 +13,7 @@ owner-side contributions (``reduce_grads``) the sum of squares is fused into the
 import math
 
 import torch
+from torch.autograd.profiler import record_function
 
 from . import ops
 
@@ -107,7 +108,8 @@ class Zero1ShardOptimizer:
         if self.shard.g.dtype != torch.bfloat16:
             raise RuntimeError('yoco_z1: reduce_grads needs a bf16 gradient shard')
         world = len(contribs)
-        ops.owner_sum(contribs, self.shard.g, 1.0 / world if scale is None else scale, partials=self._partials)
+        with record_function('reduce-grads'):        # the reference's profiler region (trainer_nosync.py:268)
+            ops.owner_sum(contribs, self.shard.g, 1.0 / world if scale is None else scale, partials=self._partials)
         # the fused partials cover the whole flat buffer; with alignment gaps the norm is taken over the table
         self._partials_ready = self.shard.total == self.shard.numel
 

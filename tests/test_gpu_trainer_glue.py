@@ -108,3 +108,19 @@ def test_pending_semantics(pkg, dev):
     torch.cuda.synchronize()
     with pytest.raises(FloatingPointError, match='Nan/Inf'):
         p.check(block=False)
+
+
+def test_profiler_regions_carry_the_reference_names(pkg, dev):
+    """trainer_nosync.py:268,273,281,288 name the phases for torch's profiler; the same names appear here."""
+    from torch.profiler import ProfilerActivity, profile
+    from faster_yoco_amd import shard as shard_mod, trainer_glue
+    sh16 = shard_mod.FlatShard([(64, 64), (64,)], dev, grad_dtype=torch.bfloat16)
+    opt = shard_mod.Zero1ShardOptimizer(sh16, **HP)
+    upd = trainer_glue.TrainerUpdate(opt, clip_norm=1.0, numer=8)
+    contribs = [torch.zeros(sh16.total, dtype=torch.bfloat16, device=dev) for _ in range(8)]
+    with profile(activities=[ProfilerActivity.CPU]) as prof:
+        opt.reduce_grads(contribs)
+        upd(torch.tensor([2048.0], device=dev))
+    torch.cuda.synchronize()
+    names = {e.name for e in prof.events()}
+    assert {'reduce-grads', 'clip-grads', 'optimizer'} <= names
