@@ -56,7 +56,8 @@ typedef struct z1_tensor {
 typedef struct z1_table z1_table;            /* opaque, device-resident table + chunk schedule */
 
 /* Builds the device copy of `rows` (plain copy of the pointers; rows with n == 0 are dropped) on the current
- * device.  Replaces the per-call tensor-list walk of yoco/tasks/fused_adam_cast.py:62-72 and the bucket/view
+ * device.  The p, m, v and p16 ranges of different rows must not overlap (each element is updated by exactly one
+ * lane; overlapping rows race).  Replaces the per-call tensor-list walk of yoco/tasks/fused_adam_cast.py:62-72 and the bucket/view
  * bookkeeping of yoco/tasks/zero1_fast.py:110-128 with one schedule built at set-up.  Allocates (hipMalloc). */
 int z1_table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table** out);
 int z1_table_destroy(z1_table* table);
