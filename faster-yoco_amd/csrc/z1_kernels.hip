@@ -41,6 +41,7 @@
 #include <vector>
 
 #include "yoco_z1.h"
+#include "z1_internal.h"
 
 #pragma clang fp contract(off)
 
@@ -565,6 +566,7 @@ int cu_count(int dev, int* cus) {
 // per CU: Adam 2.081 -> 2.038 ms at 16 one-wave workgroups per CU instead of the 32 the waves allow; 13 or fewer
 // and 20 or more are slower).  0 when the device does not report its LDS size.
 int occupancy_lds(int dev, int per_cu, size_t* bytes) {
+    if (dev < 0 || dev >= kMaxDevices || per_cu < 1) return Z1_E_DEVICE;
     std::lock_guard<std::mutex> lk(g_mu);
     if (g_dev[dev].lds_per_cu < 0) {
         int v = 0;
@@ -606,6 +608,10 @@ struct z1_table {
     int64_t numel;
     int64_t nchunks;
 };
+
+namespace z1detail {
+int occupancy_lds(int dev, int per_cu, size_t* bytes) { return ::occupancy_lds(dev, per_cu, bytes); }
+}  // namespace z1detail
 
 extern "C" {
 
