@@ -316,7 +316,8 @@ def main():
         'achieved_GBps': round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
         'frac_of_peak': round(step_bytes / (ms_step * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
         'kernel_ms': {'adam_cast': round(adam_avg, 4),
-                      ('owner_sum+norm_clip' if cfg == 'c3' else 'sumsq+norm_clip'): round(sum(pre_ms) / len(pre_ms), 4)},
+                      ('owner_sum+norm_clip' if cfg == 'c3' else 'sumsq+norm_clip'):
+                          round(sum(pre_ms) / len(pre_ms), 4)},
         'roofline': {'bound': 'hbm', 'kernel': 'adam_cast_kernel', 'achieved': round(achieved, 1),
                      'peak': PEAK_HBM_GBPS, 'unit': 'GB/s', 'frac': round(achieved / PEAK_HBM_GBPS, 4),
                      'traffic': load_traffic('adam_cast', cfg),

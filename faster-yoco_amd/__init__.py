@@ -15,4 +15,5 @@ Modules
 """
 from . import _lib, ops  # noqa: F401
 
-__all__ = ['ops', 'shard', 'fused_adam_cast', 'zero1_fast', 'ce_reduce', 'configs', 'layout', 'trainer_glue', 'embedding']
+__all__ = ['ops', 'shard', 'fused_adam_cast', 'zero1_fast', 'ce_reduce', 'configs', 'layout', 'trainer_glue',
+           'embedding']

@@ -216,4 +216,5 @@ def ulp_diff_f32(a, b):
 
 
 __all__ = ['bf16_rne', 'bf16_to_f32', 'owner_sum', 'sum_slots', 'scale_up', 'sumsq', 'norm_clip', 'clip_factor',
-           'update_scalars', 'bias_corrections', 'adam_cast', 'embedding_backward', 'greedy_partition', 'ulp_diff_f32', 'build', 'lib']
+           'update_scalars', 'bias_corrections', 'adam_cast', 'embedding_backward', 'greedy_partition',
+           'ulp_diff_f32', 'build', 'lib']
