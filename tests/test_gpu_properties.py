@@ -11,7 +11,7 @@ import oracle
 
 pytestmark = pytest.mark.gpu
 
-SETTINGS = settings(max_examples=40, deadline=None, suppress_health_check=list(HealthCheck), derandomize=True)
+SETTINGS = settings(max_examples=200, deadline=None, suppress_health_check=list(HealthCheck), derandomize=True)
 
 
 def place(arr, off, dev, bf16=False):
