@@ -1,4 +1,4 @@
-"""Parity at the BASELINE sizes (C2 431M shard, C3 8-contribution owner reduce, C4 3.45B unsharded, C5 heavy tails).
+"""Parity at the benchmark sizes (C2 431M shard, C3 8-contribution owner reduce, C4 3.45B unsharded, C5 heavy tails).
 
 At these sizes the oracle checks what it can in seconds:
   * Adam / BF16: bit-exact against the oracle on ~1M sampled elements (plus the first and last elements of every
