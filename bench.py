@@ -2,7 +2,8 @@
 
 A step is one optimizer update of one GPU's shard with its inputs resident in HBM: sum of squares -> norm + clip
 factor -> Adam + BF16 copy (config c3 adds the fused owner sum of 8 BF16 contributions in front, replacing the
-sum of squares).  Default workload: c2, the 430,662,912-parameter YOCO-3B shard (the configuration the metric is quoted on).
+sum of squares).  Default workload: c2, the 430,662,912-parameter YOCO-3B shard (the configuration the metric is
+quoted on).
 
 Prints ONE JSON line: ms per step (the metric), the Adam kernel's roofline from HIP events recorded on the
 launch stream, and the PyTorch-CPU restatement's time on a bounded sample of the same workload.
