@@ -48,7 +48,8 @@ def load_traffic(kernel, workload):
 
 def cpu_baseline(shard, cfg, ntensors, contribs, hp, step, threads):
     """Times the PyTorch-CPU restatement (oracle/torch_cpu.py) on the first `ntensors` tensors of the same shard
-    (copied from the GPU buffers), 1 warm-up + median of 5, scaled to the whole shard by parameter count."""
+    (copied from the GPU buffers), 1 warm-up + the median of the timed runs (at least 5, until ~10 s of timed work,
+    at most 25), scaled to the whole shard by parameter count."""
     import torch
     sys.path.insert(0, ROOT)
     from oracle import torch_cpu
@@ -64,7 +65,9 @@ def cpu_baseline(shard, cfg, ntensors, contribs, hp, step, threads):
         return [buf[o:o + n] for o, n in zip(shard.offsets[:k], shard.numels[:k])]
 
     times = []
-    for it in range(6):
+    for it in range(26):           # 1 warm-up, then timed runs until ~10 s of timed work (at least 5, at most 25)
+        if it > 5 and sum(times) >= 10.0:
+            break
         p, m, v = host['p'].clone(), host['m'].clone(), host['v'].clone()
         g = g_host.clone() if g_host is not None else torch.empty(end, dtype=torch.float32)
         p16 = torch.empty(end, dtype=torch.bfloat16)
@@ -80,7 +83,8 @@ def cpu_baseline(shard, cfg, ntensors, contribs, hp, step, threads):
     return {'value': round(ms_sample * shard.numel / n_s, 3), 'unit': 'ms per full-shard step (scaled)',
             'cores': threads, 'kind': 'port',
             'sample': f'first {k} tensors of the same {cfg} shard ({n_s:,} of {shard.numel:,} params), '
-                      f'median of 5 after 1 warm-up = {ms_sample:.1f} ms, scaled by parameter count; '
+                      f'median of {len(times)} after 1 warm-up ({sum(times):.1f} s timed) = {ms_sample:.1f} ms, '
+                      f'scaled by parameter count; '
                       f'torch {torch.__version__} CPU, os.cpu_count()={os.cpu_count()}'}
 
 
