@@ -178,13 +178,18 @@ template <int GDT, int MODE>
 __global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row* __restrict__ rows,
                                                                        const int32_t* __restrict__ chunk_row,
                                                                        int64_t nchunks,
-                                                                       const float* __restrict__ factor, AdamK k) {
+                                                                       const float* __restrict__ factor,
+                                                                       const float* __restrict__ bc, AdamK k) {
     const int lane = threadIdx.x & (kWave - 1);
     // last chunk first: the end of the gradient is what the norm pass read last (still in the MALL)
     const int64_t c = nchunks - 1 - (chunk_of_block(blockIdx.x, gridDim.x) * kAdamWaves +
                                      __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
     if (c < 0) return;
     const float f = factor ? *factor : 1.0f;
+    if (bc) {                                   // bias corrections from device memory (z1_adam_cast_dev)
+        k.bc1 = bc[0];
+        k.bc2 = bc[1];
+    }
     const Row r = rows[chunk_row[c]];
     const int64_t base = (c - r.chunk0) * kChunk;
     const int64_t rem = r.n - base;
@@ -380,6 +385,21 @@ __global__ __launch_bounds__(kThreads) void update_scalars_kernel(const double* 
             u.flags_out[1] = 1;                               // one owner: consistent with itself
         }
         if (u.clip_log_out && u.max_norm > 0.0f) *u.clip_log_out = gn > u.max_norm ? 100.0f : 0.0f;
+    }
+}
+
+// The step counter and bias corrections on the device (z1_bias_corrections_step): ++*step; bc = fp32(1 - beta^step)
+// computed in double, as yoco/tasks/fused_adam_cast.py:58-60 computes them on the host.
+__global__ void bias_step_kernel(int64_t* step, double beta1, double beta2, int bias_correction, float* bc) {
+    if (threadIdx.x != 0) return;
+    const int64_t s = *step + 1;
+    *step = s;
+    if (bias_correction == 1) {
+        bc[0] = (float)(1.0 - pow(beta1, (double)s));
+        bc[1] = (float)(1.0 - pow(beta2, (double)s));
+    } else {
+        bc[0] = 1.0f;
+        bc[1] = 1.0f;
     }
 }
 
@@ -767,8 +787,8 @@ int z1_clip_factor(const float* norm, const float* factor_in, float factor_value
     return launch_status();
 }
 
-int z1_adam_cast(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
-                 float bc1, float bc2, float weight_decay, int mode, void* stream) {
+static int adam_launch(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
+                       float bc1, float bc2, const float* bc, float weight_decay, int mode, void* stream) {
     if (!table) return Z1_E_NULL;
     if (mode != 0 && mode != 1) return Z1_E_MODE;
     if (!table->has_pmv) return Z1_E_NULL;
@@ -793,7 +813,7 @@ int z1_adam_cast(const z1_table* table, const float* factor, float lr, float bet
     if (rc) return rc;
 #define Z1_LAUNCH_ADAM(GDT, MODE)                                                                              \
     hipLaunchKernelGGL((adam_cast_kernel<GDT, MODE>), grid, dim3(kWave * kAdamWaves), lds, s, table->rows,    \
-                       table->chunk_row, table->nchunks, factor, k)
+                       table->chunk_row, table->nchunks, factor, bc, k)
     if (table->g_dtype == Z1_F32) {
         if (mode == 1) Z1_LAUNCH_ADAM(Z1_F32, 1);
         else Z1_LAUNCH_ADAM(Z1_F32, 0);
@@ -802,6 +822,25 @@ int z1_adam_cast(const z1_table* table, const float* factor, float lr, float bet
         else Z1_LAUNCH_ADAM(Z1_BF16, 0);
     }
 #undef Z1_LAUNCH_ADAM
+    return launch_status();
+}
+
+int z1_adam_cast(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
+                 float bc1, float bc2, float weight_decay, int mode, void* stream) {
+    return adam_launch(table, factor, lr, beta1, beta2, eps, bc1, bc2, nullptr, weight_decay, mode, stream);
+}
+
+int z1_adam_cast_dev(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
+                     const float* bc, float weight_decay, int mode, void* stream) {
+    if (!bc) return Z1_E_NULL;
+    return adam_launch(table, factor, lr, beta1, beta2, eps, 1.0f, 1.0f, bc, weight_decay, mode, stream);
+}
+
+int z1_bias_corrections_step(int64_t* step, double beta1, double beta2, int bias_correction, float* bc,
+                             void* stream) {
+    if (!step || !bc) return Z1_E_NULL;
+    hipLaunchKernelGGL(bias_step_kernel, dim3(1), dim3(kWave), 0, static_cast<hipStream_t>(stream), step, beta1,
+                       beta2, bias_correction, bc);
     return launch_status();
 }
 

@@ -185,6 +185,29 @@ def adam_cast(table, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode
                                  stream_handle(table.device)), 'z1_adam_cast')
 
 
+def adam_cast_dev(table, factor, lr, beta1, beta2, eps, bc, weight_decay, mode):
+    """adam_cast with the bias corrections read from bc (2-element fp32 device tensor) when the kernel runs."""
+    require_gpu(bc, 'adam_cast_dev')
+    if bc.dtype != torch.float32 or bc.numel() < 2 or not bc.is_contiguous():
+        raise RuntimeError('yoco_z1: bias corrections must be a contiguous 2-element fp32 tensor')
+    with torch.cuda.device(table.device):
+        check(lib().z1_adam_cast_dev(table.handle, _scalar(factor, 'adam_cast_dev'), f32(lr), f32(beta1), f32(beta2),
+                                     f32(eps), ptr(bc), f32(weight_decay), int(mode), stream_handle(table.device)),
+              'z1_adam_cast_dev')
+
+
+def bias_corrections_step(step, beta1, beta2, bc, bias_correction=1):
+    """On the device: step += 1, bc = fp32(1 - beta**step) in double (yoco/tasks/fused_adam_cast.py:58-60).
+    step: 1-element int64 device tensor; bc: 2-element fp32 device tensor."""
+    for t, what in ((step, 'step'), (bc, 'bc')):
+        require_gpu(t, 'bias_corrections_step')
+    if step.dtype != torch.int64 or bc.dtype != torch.float32 or bc.numel() < 2:
+        raise RuntimeError('yoco_z1: bias_corrections_step takes an int64 step and a 2-element fp32 bc')
+    with torch.cuda.device(step.device):
+        check(lib().z1_bias_corrections_step(ptr(step), float(beta1), float(beta2), int(bias_correction), ptr(bc),
+                                             stream_handle(step.device)), 'z1_bias_corrections_step')
+
+
 def owner_sum(contribs, out, scale, out_sum=None, partials=None):
     """out[e] = bf16(sum_k float(contribs[k][e]) * scale), k in list order.  contribs: bf16 tensors (or raw
     device addresses as ints) of out.numel() elements each; out may be one of them."""

@@ -79,7 +79,7 @@ class Zero1ShardOptimizer:
     """
 
     def __init__(self, shard, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, adam_w_mode=True,
-                 bias_correction=True):
+                 bias_correction=True, device_step=False):
         self.shard = shard
         self.lr = float(lr)
         self.betas = (float(betas[0]), float(betas[1]))
@@ -95,6 +95,11 @@ class Zero1ShardOptimizer:
         self._factor = torch.ones(1, dtype=torch.float32, device=dev)
         self._norm = torch.zeros(1, dtype=torch.float32, device=dev)
         self._partials_ready = False
+        # device_step: the step counter and bias corrections live on the device and the step advances there, so
+        # an update captured once in a HIP graph replays correctly at every step (step_count counts host calls)
+        self.device_step = bool(device_step)
+        self._step_dev = torch.zeros(1, dtype=torch.int64, device=dev) if device_step else None
+        self._bc = torch.ones(2, dtype=torch.float32, device=dev) if device_step else None
 
     # -- fairseq surface -------------------------------------------------------------------------------------
     def multiply_grads(self, c):
@@ -163,6 +168,13 @@ class Zero1ShardOptimizer:
         self._needs_sync = False
         return grad_norm.view(())
 
+    def set_step(self, n):
+        """The number of steps taken so far (the next step is n + 1), on the host and, with device_step, on the
+        device."""
+        self.step_count = int(n)
+        if self.device_step:
+            self._step_dev.fill_(int(n))
+
     def step(self, closure=None, groups=None):
         """Adam + BF16 over the shard with the gradient factor folded into the gradient load, then factor := 1."""
         self.step_count += 1
@@ -176,8 +188,13 @@ class Zero1ShardOptimizer:
         else:
             self._factor.fill_(float(factor))
             factor = self._factor
-        ops.adam_cast(self.shard.table, factor, self.lr, self.betas[0], self.betas[1], self.eps, bc1, bc2,
-                      self.weight_decay, self.mode)
+        if self.device_step:
+            ops.bias_corrections_step(self._step_dev, self.betas[0], self.betas[1], self._bc, self.bias_correction)
+            ops.adam_cast_dev(self.shard.table, factor, self.lr, self.betas[0], self.betas[1], self.eps, self._bc,
+                              self.weight_decay, self.mode)
+        else:
+            ops.adam_cast(self.shard.table, factor, self.lr, self.betas[0], self.betas[1], self.eps, bc1, bc2,
+                          self.weight_decay, self.mode)
         self._multiply_factor = 1.0
         self._needs_sync = False
 

@@ -120,6 +120,20 @@ int z1_clip_factor(const float* norm, const float* factor_in, float factor_value
 int z1_adam_cast(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
                  float bc1, float bc2, float weight_decay, int mode, void* stream);
 
+/* z1_adam_cast with bc1 = bc[0] and bc2 = bc[1] read from device memory when the kernel runs (bc: device float[2],
+ * e.g. from z1_bias_corrections_step), so that an update captured once in a HIP graph can be replayed at every
+ * step.  No counterpart in the reference, whose host rounds the corrections at each call
+ * (yoco/tasks/fused_adam_cast.py:58-60); the values are the same. */
+int z1_adam_cast_dev(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
+                     const float* bc, float weight_decay, int mode, void* stream);
+
+/* The step counter and bias corrections on the device, for z1_adam_cast_dev: ++*step, then
+ * bc[0] = fp32(1 - pow(beta1, *step)), bc[1] = fp32(1 - pow(beta2, *step)) in double (bias_correction != 1:
+ * 1, 1) -- yoco/tasks/fused_adam_cast.py:58-60 with FusedAdamV2's group['step'] += 1, on the device.  step: device
+ * int64; bc: device float[2]. */
+int z1_bias_corrections_step(int64_t* step, double beta1, double beta2, int bias_correction, float* bc,
+                             void* stream);
+
 /* g32[i] = fp32(float(g16[i]) * factor[0]) (yoco/tasks/fused_adam_cast.py:75-89). */
 int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n, void* stream);
 

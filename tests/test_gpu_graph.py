@@ -91,3 +91,62 @@ def test_update_graph_replays_match_eager(pkg, dev, form):
         check_same(sh, ref)
         del junk
     graph.reset()
+
+
+def test_device_step_graph_replays_every_step(pkg, dev):
+    """With device_step the step counter and bias corrections advance on the device, so one captured update
+    replays correctly at every step: each replay (new gradients written between them, as a backward pass would)
+    equals the eager update at the next step, with the host-rounded corrections."""
+    from faster_yoco_amd import configs, shard as shard_mod
+    sh_a, _ = make(dev, configs.C1_MINI_SHAPES, torch.float32, seed=31, step=1)
+    sh_b, opt_b = make(dev, configs.C1_MINI_SHAPES, torch.float32, seed=31, step=1)
+    opt_a = shard_mod.Zero1ShardOptimizer(sh_a, **HP, device_step=True)
+    opt_a.set_step(41)
+    opt_b.set_step(41)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gn_graph = opt_a.update(1.0)
+    torch.cuda.synchronize()
+    rng = np.random.default_rng(32)
+    for rep in range(3):
+        g = torch.from_numpy((rng.standard_normal(sh_a.total) * 3e-3).astype(np.float32)).to(dev)
+        sh_a.g.copy_(g)
+        sh_b.g.copy_(g)
+        graph.replay()
+        gn_eager = opt_b.update(1.0)
+        torch.cuda.synchronize()
+        assert torch.equal(bits(gn_graph.reshape(1)), bits(gn_eager.reshape(1))), rep
+        check_same(sh_a, state(sh_b))
+    assert int(opt_a._step_dev.item()) == 44 and opt_b.step_count == 44
+    graph.reset()
+
+
+def state(sh):
+    return {k: getattr(sh, k).clone() for k in ('p', 'm', 'v', 'p16')}
+
+
+def test_device_bias_corrections_equal_host_rounding(pkg, dev):
+    """z1_bias_corrections_step's fp32(1 - beta^step), computed in double on the device, equals the host's
+    (yoco/tasks/fused_adam_cast.py:58-60) at every step 1..20000 for two beta pairs, and at large steps."""
+    from faster_yoco_amd import ops
+    for b1, b2 in ((0.9, 0.95), (0.9, 0.999)):
+        step = torch.zeros(1, dtype=torch.int64, device=dev)
+        bc = torch.empty(2, dtype=torch.float32, device=dev)
+        n = 20000
+        rec = torch.empty(n, 2, dtype=torch.float32, device=dev)
+        for i in range(n):
+            ops.bias_corrections_step(step, b1, b2, bc)
+            rec[i].copy_(bc)
+        got = rec.cpu().numpy()
+        want = np.array([ops.bias_corrections(b1, b2, s) for s in range(1, n + 1)], dtype=np.float32)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (b1, b2)
+        assert int(step.item()) == n
+        for s in (10 ** 6, 10 ** 7, 2 ** 31, 10 ** 9):
+            step.fill_(s - 1)
+            ops.bias_corrections_step(step, b1, b2, bc)
+            assert tuple(bc.cpu().numpy()) == tuple(np.float32(ops.bias_corrections(b1, b2, s))), s
+    step = torch.zeros(1, dtype=torch.int64, device=dev)
+    bc = torch.zeros(2, dtype=torch.float32, device=dev)
+    ops.bias_corrections_step(step, 0.9, 0.95, bc, bias_correction=0)
+    assert bc.tolist() == [1.0, 1.0]
