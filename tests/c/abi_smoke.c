@@ -17,6 +17,8 @@ int main(void) {
     memset(&u, 0, sizeof(u));
     bad |= z1_update_scalars_run(0, &u, 0) != Z1_E_NULL;
     bad |= z1_embedding_backward_workspace(-1, 10) != Z1_E_SIZE;
+    bad |= z1_adam_cast_dev(0, 0, 0.f, 0.f, 0.f, 0.f, 0, 0.f, 1, 0) != Z1_E_NULL;
+    bad |= z1_bias_corrections_step(0, 0.9, 0.95, 1, 0, 0) != Z1_E_NULL;
     printf("%s\n", bad ? "FAIL" : "ok");
     return bad;
 }
