@@ -7,20 +7,23 @@
 //     the same device allocation, so a wave finds its row with two scalar loads.
 //   * Adam + BF16: one wave per chunk, one wave per workgroup, dispatched by the hardware (grid = chunks).  The
 //     workgroup -> chunk map undoes the round-robin dispatch over the 8 XCDs, so each XCD streams one contiguous
-//     eighth of the shard.  Measured on MI355X (431M-element shard): 2.10 ms, against 2.52 ms for a persistent
-//     grid with a static partition (tail imbalance across CUs/XCDs) and 2.19 ms for 1024-element workgroups; the
-//     same kernel with its arithmetic replaced by additions runs at the same speed, i.e. it is at the bandwidth
-//     this 4-read / 4-write stream pattern reaches.
+//     eighth of the shard, taken from its last chunk down (see the MALL note below); a dynamic LDS reservation
+//     the kernel does not touch caps it at 16 resident workgroups per CU.  Measured on MI355X (431M-element
+//     shard): 2.05 ms on typical boxes, against 2.52 ms for a persistent grid with a static partition (tail
+//     imbalance across CUs/XCDs) and 2.19 ms for 1024-element workgroups; the same kernel with its arithmetic
+//     replaced by additions runs at the same speed, i.e. it is at the bandwidth this 4-read / 4-write stream
+//     pattern reaches.
 //   * Each lane moves one 128-bit group per fp32 array (and 64 bits of bf16); a wave instruction covers 1 KiB
 //     (fp32) or 512 B (bf16) of contiguous bytes, with nontemporal hints (streams far larger than L2 and MALL).
 //     The last, partial chunk of a row (and rows whose pointers are not aligned for the vector path) run an
 //     element-wise loop.
-//   * The norm uses the same table and a FIXED grid (Z1_NORM_PARTIALS workgroups of 4 waves; workgroup b takes
-//     chunks 4b..4b+3, then 4(b+G).., i.e. 1024 contiguous elements per step), FP64 accumulation of the exact
-//     squares per lane, a wave64 xor-butterfly and a fixed-order LDS stage: its bits do not depend on timing, on
-//     the device's CU count or on the run.  Measured 0.27 ms for the 1.72 GB gradient (6.4 TB/s); one wave per
-//     chunk with hardware dispatch (0.40 ms), 4-chunk workgroups with hardware dispatch (0.34 ms) and 2-8 loads
-//     in flight per wave (0.28-0.31 ms) were all slower.
+//   * The norm uses the same table and a FIXED grid of Z1_NORM_PARTIALS workgroups of 4 waves, split by XCD: the
+//     256 workgroups dispatched to one XCD stride through that XCD's eighth of the chunks, 1024 contiguous
+//     elements per workgroup step.  FP64 accumulation of the exact squares per lane, a wave64 xor-butterfly and
+//     a fixed-order LDS stage: its bits do not depend on timing, on the device's CU count or on the run.
+//     Measured 0.25 ms for the 1.72 GB gradient (6.8 TB/s); the grid striding over all chunks (0.27 ms), one
+//     wave per chunk with hardware dispatch (0.40 ms), 4-chunk workgroups with hardware dispatch (0.34 ms),
+//     2-8 loads in flight per wave (0.28-0.31 ms) and fewer waves (0.35-0.59 ms) were all slower.
 //   * MALL reuse between passes: the pass before Adam (the norm, or the owner sum that writes the BF16 average)
 //     touches the last kMallKeepBytes of the gradient with ordinary, allocating accesses, and Adam walks the
 //     chunks from the last one, so its first gradient reads hit the 256 MB MALL (measured 2.05 vs 2.10 ms for
