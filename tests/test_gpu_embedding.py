@@ -41,6 +41,21 @@ def test_matches_aten_sort_path(pkg, dev, padding_idx, D):
     assert np.array_equal(bits(got2), bits(ref2)) and np.array_equal(bits(got3), bits(ref3))
 
 
+@pytest.mark.parametrize('R', [65536, 1_500_000])
+def test_matches_aten_at_larger_row_counts(pkg, dev, R):
+    """More rows than the recipe's 16,384: the sort runs rocPRIM's other algorithms (merge sort up to 1M items,
+    onesweep above); still bit-exact against aten."""
+    from faster_yoco_amd import embedding
+    rng = np.random.default_rng(R)
+    V, D = 100288, 64
+    ids = torch.from_numpy(zipf_ids(rng, R, V)).to(dev)
+    g = (torch.randn(R, D, device=dev) * 1e-2).to(torch.bfloat16)
+    ref = torch.ops.aten.embedding_dense_backward(g, ids, V, -1, False)
+    got = embedding.embedding_dense_backward(g, ids, V, -1)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(got), bits(ref))
+
+
 def test_matches_oracle_and_edge_cases(pkg, dev):
     from faster_yoco_amd import embedding
     rng = np.random.default_rng(3)
