@@ -11,7 +11,10 @@
 //   3. row_lo[t] = start of id t's run in the sorted keys (one binary search per t, all in parallel);
 //   4. one wave per output row t writes the row's sums -- or zeros -- exactly once, 8 bf16 columns per lane, with
 //      nontemporal stores (aten zero-fills the whole table and then scatters into it; here every row of the table
-//      is written once).  Measured: 4 rows per 256-thread workgroup instead of one wave per row, no difference.
+//      is written once), for ids with at most kHeavyRows occurrences; the others are listed for
+//   5. emb_heavy_kernel, which forms a heavy id's partials of 10 in parallel (16 per workgroup batch) and adds
+//      them in order: token frequencies in text are skewed, and one wave walking thousands of occurrences of one
+//      id would take milliseconds.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
@@ -29,6 +32,10 @@ constexpr int kRowsPerPartial = 10;        // aten's NROWS_PER_THREAD
 // resident row workgroups per CU, capped with a dynamic LDS reservation the kernel does not use: 0.131 ms per call
 // at 9-10 per CU against 0.148 ms at the 32 the waves allow (0.144 at 16, 0.136 at 8, 0.146 at 7, 0.180 at 6)
 constexpr int kEmbWgPerCu = 10;
+constexpr int kWave = 64;
+constexpr int kHeavyRows = 20;             // tokens with more occurrences go to emb_heavy_kernel
+constexpr int kHeavyWaves = 16;            // waves of a heavy workgroup: one run partial each per batch
+constexpr int kHeavyGrid = 1024;           // heavy workgroups (each loops over the heavy items)
 
 __device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
@@ -50,8 +57,9 @@ __global__ void emb_keys_kernel(const int64_t* __restrict__ ids, int64_t R, int6
 // row_lo[t] = first index of the sorted keys that is >= t, for t in [0, V]: row t's occurrences are
 // [row_lo[t], row_lo[t+1]).  One independent binary search per thread (the latency of the searches overlaps).
 __global__ void emb_row_ranges_kernel(const uint32_t* __restrict__ sorted, int64_t R, int64_t V,
-                                      int32_t* __restrict__ row_lo) {
+                                      int32_t* __restrict__ row_lo, int* __restrict__ heavy_count) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t == 0) *heavy_count = 0;               // the rows kernel appends the heavy tokens after this kernel
     if (t > V) return;
     int64_t lo = 0, hi = R;
     while (lo < hi) {
@@ -64,14 +72,38 @@ __global__ void emb_row_ranges_kernel(const uint32_t* __restrict__ sorted, int64
 
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-// One wave per output row t.  scale_mode 0: none; 1: each gradient element first rounded to bf16(g * scale) (the
-// CE path scales the staged rows in place, ce_reduce.py:228); 2: the finished bf16 sum multiplied by scale and
-// rounded again (layer_graphs.py:93).  vec: D % 8 == 0 and both tables 16-byte aligned (8 columns per lane).
+// One gradient element as it enters a partial: scale_mode 1 rounds bf16(g * scale) first (the CE path scales the
+// staged rows in place, ce_reduce.py:228).
+__device__ __forceinline__ float grad_elem(uint16_t h, float scale, int scale_mode) {
+    float v = bf16f(h);
+    if (scale_mode == 1) v = bf16f(bf16r(v * scale));
+    return v;
+}
+
+// The finished fp32 sum to bf16; scale_mode 2 multiplies the bf16 result by scale and rounds again
+// (layer_graphs.py:93).
+__device__ __forceinline__ uint16_t finish(float acc, float scale, int scale_mode) {
+    uint16_t o = bf16r(acc);
+    if (scale_mode == 2) o = bf16r(bf16f(o) * scale);
+    return o;
+}
+
+__device__ __forceinline__ void nt_store(u4* p, u4 x) {
+    __builtin_nontemporal_store(x, (__attribute__((address_space(1))) u4*)p);
+}
+
+// One wave per output row t (light tokens: at most kHeavyRows occurrences, and empty or padding rows): the row's
+// sums -- or zeros -- written once, 8 bf16 columns per lane when vec (D % 8 == 0, 16-byte aligned tables).  Each
+// run of up to kRowsPerPartial occurrences has its loads issued together, then is summed in order.  A token with
+// more occurrences is appended to heavy_list (its slot from an atomic counter: the order of the list only decides
+// which workgroup of emb_heavy_kernel takes it) and its row is left to that kernel.
 __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* __restrict__ grad, int64_t D,
                                                                const int32_t* __restrict__ spos,
                                                                const int32_t* __restrict__ row_lo,
                                                                int64_t padding_idx, float scale, int scale_mode,
-                                                               int vec, uint16_t* __restrict__ out) {
+                                                               int vec, uint16_t* __restrict__ out,
+                                                               int* __restrict__ heavy_count,
+                                                               int32_t* __restrict__ heavy_list) {
     // row of workgroup b: undoes the round-robin dispatch over the 8 XCDs, so each XCD writes one contiguous
     // eighth of the table (0.148 vs 0.153 ms per call for t = b)
     int64_t t;
@@ -80,68 +112,156 @@ __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* _
         const int64_t x = b & 7, q = b >> 3, Q = nb >> 3, R = nb & 7;
         t = x * Q + (x < R ? x : R) + q;
     }
+    const int lane = threadIdx.x;
     uint16_t* orow = out + t * D;
     const int64_t lo = row_lo[t], hi = row_lo[t + 1];
     const bool empty = lo == hi || t == padding_idx;
+    if (!empty && hi - lo > kHeavyRows) {
+        if (lane == 0) heavy_list[atomicAdd(heavy_count, 1)] = (int32_t)t;
+        return;
+    }
     if (vec) {
         const int64_t ng = D / 8;
-        for (int64_t gi = threadIdx.x; gi < ng; gi += kEmbThreads) {
+        for (int64_t gi = lane; gi < ng; gi += kEmbThreads) {
             u4 o = u4{0u, 0u, 0u, 0u};
             if (!empty) {
                 float acc[8];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) acc[k] = 0.0f;
                 for (int64_t j0 = lo; j0 < hi; j0 += kRowsPerPartial) {
-                    const int64_t j1 = j0 + kRowsPerPartial < hi ? j0 + kRowsPerPartial : hi;
+                    const int cnt = (int)(j0 + kRowsPerPartial < hi ? kRowsPerPartial : hi - j0);
+                    u4 x[kRowsPerPartial];
+#pragma unroll
+                    for (int u = 0; u < kRowsPerPartial; ++u)
+                        if (u < cnt) x[u] = reinterpret_cast<const u4*>(grad + (int64_t)spos[j0 + u] * D)[gi];
                     float part[8];
 #pragma unroll
                     for (int k = 0; k < 8; ++k) part[k] = 0.0f;
-                    for (int64_t j = j0; j < j1; ++j) {
-                        const u4 x = reinterpret_cast<const u4*>(grad + (int64_t)spos[j] * D)[gi];
 #pragma unroll
-                        for (int k = 0; k < 8; ++k) {
-                            const uint16_t h = (uint16_t)(x[k >> 1] >> ((k & 1) * 16));
-                            float v = bf16f(h);
-                            if (scale_mode == 1) v = bf16f(bf16r(v * scale));
-                            part[k] = part[k] + v;
+                    for (int u = 0; u < kRowsPerPartial; ++u) {
+                        if (u < cnt) {
+#pragma unroll
+                            for (int k = 0; k < 8; ++k)
+                                part[k] = part[k] + grad_elem((uint16_t)(x[u][k >> 1] >> ((k & 1) * 16)), scale,
+                                                              scale_mode);
                         }
                     }
 #pragma unroll
                     for (int k = 0; k < 8; ++k) acc[k] = acc[k] + part[k];
                 }
 #pragma unroll
-                for (int k = 0; k < 8; k += 2) {
-                    uint16_t a = bf16r(acc[k]), b = bf16r(acc[k + 1]);
-                    if (scale_mode == 2) {
-                        a = bf16r(bf16f(a) * scale);
-                        b = bf16r(bf16f(b) * scale);
-                    }
-                    o[k >> 1] = (uint32_t)a | ((uint32_t)b << 16);
-                }
+                for (int k = 0; k < 8; k += 2)
+                    o[k >> 1] = (uint32_t)finish(acc[k], scale, scale_mode) |
+                                ((uint32_t)finish(acc[k + 1], scale, scale_mode) << 16);
             }
             // nontemporal: the 616 MB table is written once and not read back here (0.155 vs 0.184 ms per call)
-            __builtin_nontemporal_store(o, (__attribute__((address_space(1))) u4*)(reinterpret_cast<u4*>(orow) + gi));
+            nt_store(reinterpret_cast<u4*>(orow) + gi, o);
         }
         return;
     }
-    for (int64_t d = threadIdx.x; d < D; d += kEmbThreads) {
+    for (int64_t d = lane; d < D; d += kEmbThreads) {
         uint16_t o = 0;
         if (!empty) {
             float acc = 0.0f;
             for (int64_t j0 = lo; j0 < hi; j0 += kRowsPerPartial) {
                 const int64_t j1 = j0 + kRowsPerPartial < hi ? j0 + kRowsPerPartial : hi;
                 float part = 0.0f;
-                for (int64_t j = j0; j < j1; ++j) {
-                    float v = bf16f(grad[(int64_t)spos[j] * D + d]);
-                    if (scale_mode == 1) v = bf16f(bf16r(v * scale));
-                    part = part + v;
-                }
+                for (int64_t j = j0; j < j1; ++j) part = part + grad_elem(grad[(int64_t)spos[j] * D + d], scale,
+                                                                          scale_mode);
                 acc = acc + part;
             }
-            o = bf16r(acc);
-            if (scale_mode == 2) o = bf16r(bf16f(o) * scale);
+            o = finish(acc, scale, scale_mode);
         }
         orow[d] = o;
+    }
+}
+
+// Heavy tokens (more than kHeavyRows occurrences): workgroup g takes the items g, g + G, ... of (heavy token,
+// column group) -- 512 columns per group on the vector path, 64 otherwise -- until the count the rows kernel
+// left; every workgroup exits.  Per batch, wave w forms the partial of run b + w (its loads issued together,
+// summed in order) into LDS, then wave 0 adds the batch's partials to its accumulator in run order: the same
+// order as the rows kernel and aten, with the runs of one token computed in parallel.
+template <int VEC>
+__global__ __launch_bounds__(kWave * kHeavyWaves) void emb_heavy_kernel(const uint16_t* __restrict__ grad, int64_t D,
+                                                                         const int32_t* __restrict__ spos,
+                                                                         const int32_t* __restrict__ row_lo,
+                                                                         float scale, int scale_mode,
+                                                                         uint16_t* __restrict__ out,
+                                                                         const int* __restrict__ heavy_count,
+                                                                         const int32_t* __restrict__ heavy_list) {
+    constexpr int kCols = VEC ? 8 : 1;                       // columns per lane
+    __shared__ float parts[kHeavyWaves][kWave][kCols];
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+    const int64_t cols_per_item = (int64_t)kWave * kCols;
+    const int64_t ncg = (D + cols_per_item - 1) / cols_per_item;
+    const int64_t items = (int64_t)(*heavy_count) * ncg;
+    for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+        const int64_t t = heavy_list[item / ncg];
+        const int64_t c0 = (item % ncg) * cols_per_item + (int64_t)lane * kCols;   // this lane's first column
+        const bool valid = c0 < D;                                                 // D % 8 == 0 when VEC
+        const int64_t lo = row_lo[t], hi = row_lo[t + 1];
+        const int64_t nrun = (hi - lo + kRowsPerPartial - 1) / kRowsPerPartial;
+        float acc[kCols];
+#pragma unroll
+        for (int k = 0; k < kCols; ++k) acc[k] = 0.0f;
+        for (int64_t b = 0; b < nrun; b += kHeavyWaves) {
+            float part[kCols];
+#pragma unroll
+            for (int k = 0; k < kCols; ++k) part[k] = 0.0f;
+            const int64_t r = b + wave;
+            if (r < nrun && valid) {
+                const int64_t j0 = lo + r * kRowsPerPartial;
+                const int cnt = (int)(j0 + kRowsPerPartial < hi ? kRowsPerPartial : hi - j0);
+                if (VEC) {
+                    u4 x[kRowsPerPartial];
+#pragma unroll
+                    for (int u = 0; u < kRowsPerPartial; ++u)
+                        if (u < cnt) x[u] = *reinterpret_cast<const u4*>(grad + (int64_t)spos[j0 + u] * D + c0);
+#pragma unroll
+                    for (int u = 0; u < kRowsPerPartial; ++u) {
+                        if (u < cnt) {
+#pragma unroll
+                            for (int k = 0; k < kCols; ++k)
+                                part[k] = part[k] + grad_elem((uint16_t)(x[u][k >> 1] >> ((k & 1) * 16)), scale,
+                                                              scale_mode);
+                        }
+                    }
+                } else {
+                    uint16_t x[kRowsPerPartial];
+#pragma unroll
+                    for (int u = 0; u < kRowsPerPartial; ++u)
+                        if (u < cnt) x[u] = grad[(int64_t)spos[j0 + u] * D + c0];
+#pragma unroll
+                    for (int u = 0; u < kRowsPerPartial; ++u)
+                        if (u < cnt) part[0] = part[0] + grad_elem(x[u], scale, scale_mode);
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < kCols; ++k) parts[wave][lane][k] = part[k];
+            __syncthreads();
+            if (wave == 0) {
+                for (int w = 0; w < kHeavyWaves; ++w) {
+                    if (b + w < nrun) {
+#pragma unroll
+                        for (int k = 0; k < kCols; ++k) acc[k] = acc[k] + parts[w][lane][k];
+                    }
+                }
+            }
+            __syncthreads();
+        }
+        if (wave == 0 && valid) {
+            uint16_t* orow = out + t * D + c0;
+            if (VEC) {
+                u4 o;
+#pragma unroll
+                for (int k = 0; k < 8; k += 2)
+                    o[k >> 1] = (uint32_t)finish(acc[k], scale, scale_mode) |
+                                ((uint32_t)finish(acc[k + 1], scale, scale_mode) << 16);
+                nt_store(reinterpret_cast<u4*>(orow), o);
+            } else {
+                orow[0] = finish(acc[0], scale, scale_mode);
+            }
+        }
     }
 }
 
@@ -158,10 +278,13 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 extern "C" {
 
+// Workspace: keys, positions, sorted keys, sorted positions (R each), row_lo (V + 1), the heavy-token count and
+// list (V), then the sort's temporary storage.
 int64_t z1_embedding_backward_workspace(int64_t R, int64_t V) {
     if (R < 0 || R > INT32_MAX || V <= 0 || V > INT32_MAX - 1) return Z1_E_SIZE;
     const size_t kb = align256(sizeof(uint32_t) * (size_t)(R > 0 ? R : 1));
-    return (int64_t)(4 * kb + align256(sizeof(int32_t) * (size_t)(V + 1)) + align256(sort_temp_bytes(R)));
+    return (int64_t)(4 * kb + align256(sizeof(int32_t) * (size_t)(V + 1)) + 256 +
+                     align256(sizeof(int32_t) * (size_t)V) + align256(sort_temp_bytes(R)));
 }
 
 int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, int64_t D, int64_t V,
@@ -181,7 +304,10 @@ int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, i
     uint32_t* skeys = reinterpret_cast<uint32_t*>(w + 2 * kb);
     int32_t* svals = reinterpret_cast<int32_t*>(w + 3 * kb);
     int32_t* row_lo = reinterpret_cast<int32_t*>(w + 4 * kb);
-    void* temp = w + 4 * kb + align256(sizeof(int32_t) * (size_t)(V + 1));
+    const size_t rl = align256(sizeof(int32_t) * (size_t)(V + 1));
+    int* heavy_count = reinterpret_cast<int*>(w + 4 * kb + rl);
+    int32_t* heavy_list = reinterpret_cast<int32_t*>(w + 4 * kb + rl + 256);
+    void* temp = w + 4 * kb + rl + 256 + align256(sizeof(int32_t) * (size_t)V);
     hipError_t e = hipSuccess;
     if (R > 0) {
         hipLaunchKernelGGL(emb_keys_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, ids, R, V, keys,
@@ -195,7 +321,7 @@ int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, i
         if (e != hipSuccess) return (int)e;
     }
     hipLaunchKernelGGL(emb_row_ranges_kernel, dim3((unsigned)((V + 1 + 255) / 256)), dim3(256), 0, st, skeys, R, V,
-                       row_lo);
+                       row_lo, heavy_count);
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     const int vec = (D % 8 == 0) && ((reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
@@ -206,7 +332,15 @@ int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, i
     const int rc = z1detail::occupancy_lds(dev, kEmbWgPerCu, &lds);
     if (rc) return rc;
     hipLaunchKernelGGL(emb_rows_kernel, dim3((unsigned)V), dim3(kEmbThreads), lds, st, grad, D, svals, row_lo,
-                       padding_idx, scale, scale_mode, vec, out);
+                       padding_idx, scale, scale_mode, vec, out, heavy_count, heavy_list);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    if (vec)
+        hipLaunchKernelGGL(emb_heavy_kernel<1>, dim3(kHeavyGrid), dim3(kWave * kHeavyWaves), 0, st, grad, D, svals,
+                           row_lo, scale, scale_mode, out, heavy_count, heavy_list);
+    else
+        hipLaunchKernelGGL(emb_heavy_kernel<0>, dim3(kHeavyGrid), dim3(kWave * kHeavyWaves), 0, st, grad, D, svals,
+                           row_lo, scale, scale_mode, out, heavy_count, heavy_list);
     e = hipGetLastError();
     return e == hipSuccess ? Z1_OK : (int)e;
 }
