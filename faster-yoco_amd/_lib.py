@@ -54,7 +54,7 @@ SIGNATURES = {
     'z1_scale_up': ([_P, _P, _P, _I64, _P], _I),
     'z1_cast_bf16': ([_P, _P, _I64, _P], _I),
     'z1_embedding_backward': ([_P, _P, _I64, _I64, _I64, _I64, _F, _I, _P, _P, _I64, _P], _I),
-    'z1_embedding_backward_workspace': ([_I64, _I64], _I64),
+    'z1_embedding_backward_workspace': ([_I64, _I64, _I64], _I64),
     'z1_strerror': ([_I], ctypes.c_char_p),
 }
 

@@ -11,10 +11,13 @@
 //   3. row_lo[t] = start of id t's run in the sorted keys (one binary search per t, all in parallel);
 //   4. one wave per output row t writes the row's sums -- or zeros -- exactly once, 8 bf16 columns per lane, with
 //      nontemporal stores (aten zero-fills the whole table and then scatters into it; here every row of the table
-//      is written once), for ids with at most kHeavyRows occurrences; the others are listed for
-//   5. emb_heavy_kernel, which forms a heavy id's partials of 10 in parallel (16 per workgroup batch) and adds
-//      them in order: token frequencies in text are skewed, and one wave walking thousands of occurrences of one
-//      id would take milliseconds.
+//      is written once), for ids with at most kHeavyRows occurrences; the others are listed, with a slot range
+//      for their runs, for
+//   5. emb_heavy_parts_kernel, which forms every run partial of every heavy id in parallel over the whole chip
+//      into an fp32 workspace, and
+//   6. emb_heavy_chain_kernel, which adds each heavy id's partials in run order per column.  Token frequencies in
+//      text are skewed: one wave (or one workgroup) walking thousands of occurrences of one id would take
+//      milliseconds.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
 
@@ -33,9 +36,19 @@ constexpr int kRowsPerPartial = 10;        // aten's NROWS_PER_THREAD
 // at 9-10 per CU against 0.148 ms at the 32 the waves allow (0.144 at 16, 0.136 at 8, 0.146 at 7, 0.180 at 6)
 constexpr int kEmbWgPerCu = 10;
 constexpr int kWave = 64;
-constexpr int kHeavyRows = 20;             // tokens with more occurrences go to emb_heavy_kernel
-constexpr int kHeavyWaves = 16;            // waves of a heavy workgroup: one run partial each per batch
-constexpr int kHeavyGrid = 1024;           // heavy workgroups (each loops over the heavy items)
+// tokens with more occurrences go to the heavy passes; a heavy token's ceil(n / 10) runs are at most n / 7 for
+// n >= 21, so the run slots of all heavy tokens number at most R / 7
+constexpr int kHeavyRows = 20;
+static_assert(kHeavyRows >= 20, "the run-slot bound R / 7 needs heavy tokens of at least 21 occurrences");
+constexpr int kPartsThreads = 256;         // heavy pass 1: one run x column group per wave
+constexpr int kPartsGrid = 2048;
+constexpr int kChainWaves = 16;            // heavy pass 2: waves that load a batch of partials
+constexpr int kChainDepth = 16;            // partials per lane per batch
+constexpr int kChainRows = kChainWaves * kChainDepth;
+static_assert(kChainRows % 16 == 0, "wave 0 reads a batch 16 rows at a time");
+constexpr int kChainGrid = 512;
+constexpr int kWaveChainRuns = 32;         // heavy tokens of at most this many runs are chained by one wave
+constexpr int64_t kMaxCols = 1 << 24;      // D limit: keeps the workspace size and offsets far from overflow
 
 __device__ __forceinline__ float bf16f(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
@@ -57,9 +70,13 @@ __global__ void emb_keys_kernel(const int64_t* __restrict__ ids, int64_t R, int6
 // row_lo[t] = first index of the sorted keys that is >= t, for t in [0, V]: row t's occurrences are
 // [row_lo[t], row_lo[t+1]).  One independent binary search per thread (the latency of the searches overlaps).
 __global__ void emb_row_ranges_kernel(const uint32_t* __restrict__ sorted, int64_t R, int64_t V,
-                                      int32_t* __restrict__ row_lo, int* __restrict__ heavy_count) {
+                                      int32_t* __restrict__ row_lo, int* __restrict__ counts) {
     const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (t == 0) *heavy_count = 0;               // the rows kernel appends the heavy tokens after this kernel
+    if (t == 0) {                               // the rows kernel appends the heavy tokens after this kernel
+        counts[0] = 0;
+        counts[1] = 0;
+        counts[2] = 0;
+    }
     if (t > V) return;
     int64_t lo = 0, hi = R;
     while (lo < hi) {
@@ -95,15 +112,21 @@ __device__ __forceinline__ void nt_store(u4* p, u4 x) {
 // One wave per output row t (light tokens: at most kHeavyRows occurrences, and empty or padding rows): the row's
 // sums -- or zeros -- written once, 8 bf16 columns per lane when vec (D % 8 == 0, 16-byte aligned tables).  Each
 // run of up to kRowsPerPartial occurrences has its loads issued together, then is summed in order.  A token with
-// more occurrences is appended to heavy_list (its slot from an atomic counter: the order of the list only decides
-// which workgroup of emb_heavy_kernel takes it) and its row is left to that kernel.
+// more occurrences is appended, with the first of its nrun run slots (from counts[1]), to the list of tokens of at
+// most kWaveChainRuns runs (heavy_list / heavy_base, count counts[0]) or to that of longer ones (long_list /
+// long_base, counts[2]); run_start[slot] = the sorted position of the run's first row.  Its row is left to the heavy
+// passes.  The atomics only decide where a token's partials are kept, not how they are summed.
 __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* __restrict__ grad, int64_t D,
                                                                const int32_t* __restrict__ spos,
                                                                const int32_t* __restrict__ row_lo,
                                                                int64_t padding_idx, float scale, int scale_mode,
                                                                int vec, uint16_t* __restrict__ out,
-                                                               int* __restrict__ heavy_count,
-                                                               int32_t* __restrict__ heavy_list) {
+                                                               int* __restrict__ counts,
+                                                               int32_t* __restrict__ heavy_list,
+                                                               int32_t* __restrict__ heavy_base,
+                                                               int32_t* __restrict__ long_list,
+                                                               int32_t* __restrict__ long_base,
+                                                               int32_t* __restrict__ run_start) {
     // row of workgroup b: undoes the round-robin dispatch over the 8 XCDs, so each XCD writes one contiguous
     // eighth of the table (0.148 vs 0.153 ms per call for t = b)
     int64_t t;
@@ -117,7 +140,17 @@ __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* _
     const int64_t lo = row_lo[t], hi = row_lo[t + 1];
     const bool empty = lo == hi || t == padding_idx;
     if (!empty && hi - lo > kHeavyRows) {
-        if (lane == 0) heavy_list[atomicAdd(heavy_count, 1)] = (int32_t)t;
+        const int nrun = (int)((hi - lo + kRowsPerPartial - 1) / kRowsPerPartial);
+        int base = 0;
+        if (lane == 0) {
+            const bool wave_chain = nrun <= kWaveChainRuns;
+            const int h = atomicAdd(&counts[wave_chain ? 0 : 2], 1);
+            base = atomicAdd(&counts[1], nrun);
+            (wave_chain ? heavy_list : long_list)[h] = (int32_t)t;
+            (wave_chain ? heavy_base : long_base)[h] = base;
+        }
+        base = __shfl(base, 0);
+        for (int k = lane; k < nrun; k += kEmbThreads) run_start[base + k] = (int32_t)(lo + (int64_t)k * kRowsPerPartial);
         return;
     }
     if (vec) {
@@ -176,92 +209,134 @@ __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* _
     }
 }
 
-// Heavy tokens (more than kHeavyRows occurrences): workgroup g takes the items g, g + G, ... of (heavy token,
-// column group) -- 512 columns per group on the vector path, 64 otherwise -- until the count the rows kernel
-// left; every workgroup exits.  Per batch, wave w forms the partial of run b + w (its loads issued together,
-// summed in order) into LDS, then wave 0 adds the batch's partials to its accumulator in run order: the same
-// order as the rows kernel and aten, with the runs of one token computed in parallel.
+// Heavy tokens, pass 1: every run of 10 occurrences of every heavy token, for every column group (512 columns on
+// the vector path, 64 otherwise), is one wave's item; the wave sums the run's rows in order (loads issued together)
+// and stores the fp32 partial to its run slot of parts (parts[s * D + column]).  The run of slot s starts at sorted
+// position run_start[s], and its token is the sorted key there.  Items are spread over the whole
+// grid, so one token's thousands of runs are formed in parallel; every wave exits once the items run out.
 template <int VEC>
-__global__ __launch_bounds__(kWave * kHeavyWaves) void emb_heavy_kernel(const uint16_t* __restrict__ grad, int64_t D,
-                                                                         const int32_t* __restrict__ spos,
-                                                                         const int32_t* __restrict__ row_lo,
-                                                                         float scale, int scale_mode,
-                                                                         uint16_t* __restrict__ out,
-                                                                         const int* __restrict__ heavy_count,
-                                                                         const int32_t* __restrict__ heavy_list) {
+__global__ __launch_bounds__(kPartsThreads) void emb_heavy_parts_kernel(const uint16_t* __restrict__ grad, int64_t D,
+                                                                        const int32_t* __restrict__ spos,
+                                                                        const uint32_t* __restrict__ skeys,
+                                                                        const int32_t* __restrict__ row_lo,
+                                                                        const int32_t* __restrict__ run_start,
+                                                                        const int* __restrict__ counts, float scale,
+                                                                        int scale_mode, float* __restrict__ parts) {
     constexpr int kCols = VEC ? 8 : 1;                       // columns per lane
-    __shared__ float parts[kHeavyWaves][kWave][kCols];
+    constexpr int kWaves = kPartsThreads / kWave;
     const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
     const int64_t cols_per_item = (int64_t)kWave * kCols;
     const int64_t ncg = (D + cols_per_item - 1) / cols_per_item;
-    const int64_t items = (int64_t)(*heavy_count) * ncg;
-    for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
-        const int64_t t = heavy_list[item / ncg];
-        const int64_t c0 = (item % ncg) * cols_per_item + (int64_t)lane * kCols;   // this lane's first column
-        const bool valid = c0 < D;                                                 // D % 8 == 0 when VEC
-        const int64_t lo = row_lo[t], hi = row_lo[t + 1];
-        const int64_t nrun = (hi - lo + kRowsPerPartial - 1) / kRowsPerPartial;
-        float acc[kCols];
+    const int64_t items = (int64_t)counts[1] * ncg;
+    for (int64_t item = (int64_t)blockIdx.x * kWaves + wave; item < items; item += (int64_t)gridDim.x * kWaves) {
+        const int64_t s = item / ncg;
+        const int64_t c0 = (item % ncg) * cols_per_item + (int64_t)lane * kCols;   // D % 8 == 0 when VEC
+        if (c0 >= D) continue;
+        const int64_t j0 = run_start[s];
+        const int64_t hi = row_lo[(int64_t)skeys[j0] + 1];
+        const int cnt = (int)(j0 + kRowsPerPartial < hi ? kRowsPerPartial : hi - j0);
+        float part[kCols];
 #pragma unroll
-        for (int k = 0; k < kCols; ++k) acc[k] = 0.0f;
-        for (int64_t b = 0; b < nrun; b += kHeavyWaves) {
-            float part[kCols];
+        for (int k = 0; k < kCols; ++k) part[k] = 0.0f;
+        if (VEC) {
+            u4 x[kRowsPerPartial];
 #pragma unroll
-            for (int k = 0; k < kCols; ++k) part[k] = 0.0f;
-            const int64_t r = b + wave;
-            if (r < nrun && valid) {
-                const int64_t j0 = lo + r * kRowsPerPartial;
-                const int cnt = (int)(j0 + kRowsPerPartial < hi ? kRowsPerPartial : hi - j0);
-                if (VEC) {
-                    u4 x[kRowsPerPartial];
+            for (int u = 0; u < kRowsPerPartial; ++u)
+                if (u < cnt) x[u] = *reinterpret_cast<const u4*>(grad + (int64_t)spos[j0 + u] * D + c0);
 #pragma unroll
-                    for (int u = 0; u < kRowsPerPartial; ++u)
-                        if (u < cnt) x[u] = *reinterpret_cast<const u4*>(grad + (int64_t)spos[j0 + u] * D + c0);
+            for (int u = 0; u < kRowsPerPartial; ++u) {
+                if (u < cnt) {
 #pragma unroll
-                    for (int u = 0; u < kRowsPerPartial; ++u) {
-                        if (u < cnt) {
-#pragma unroll
-                            for (int k = 0; k < kCols; ++k)
-                                part[k] = part[k] + grad_elem((uint16_t)(x[u][k >> 1] >> ((k & 1) * 16)), scale,
-                                                              scale_mode);
-                        }
-                    }
-                } else {
-                    uint16_t x[kRowsPerPartial];
-#pragma unroll
-                    for (int u = 0; u < kRowsPerPartial; ++u)
-                        if (u < cnt) x[u] = grad[(int64_t)spos[j0 + u] * D + c0];
-#pragma unroll
-                    for (int u = 0; u < kRowsPerPartial; ++u)
-                        if (u < cnt) part[0] = part[0] + grad_elem(x[u], scale, scale_mode);
+                    for (int k = 0; k < kCols; ++k)
+                        part[k] = part[k] + grad_elem((uint16_t)(x[u][k >> 1] >> ((k & 1) * 16)), scale, scale_mode);
                 }
             }
+        } else {
+            uint16_t x[kRowsPerPartial];
 #pragma unroll
-            for (int k = 0; k < kCols; ++k) parts[wave][lane][k] = part[k];
+            for (int u = 0; u < kRowsPerPartial; ++u)
+                if (u < cnt) x[u] = grad[(int64_t)spos[j0 + u] * D + c0];
+#pragma unroll
+            for (int u = 0; u < kRowsPerPartial; ++u)
+                if (u < cnt) part[0] = part[0] + grad_elem(x[u], scale, scale_mode);
+        }
+        float* dst = parts + s * D + c0;
+#pragma unroll
+        for (int k = 0; k < kCols; ++k) dst[k] = part[k];
+    }
+}
+
+// Heavy tokens, pass 2: each (heavy token, 64 columns) is an item, one column per lane, whose partials are added in
+// run order -- the order of the rows kernel and of aten -- and rounded to the bf16 row.
+//   - tokens of more than kWaveChainRuns runs (long_list): workgroup g takes the items g, g + G, ...; per batch its
+//     waves load the token's next kChainRows partials into LDS (kChainDepth loads in flight per lane), then wave 0
+//     adds them to its accumulator;
+//   - the others (heavy_list): wave w of the grid takes the items w, w + W, ..., loads all of the token's partials
+//     at once and adds them in registers, with no barrier.
+__global__ __launch_bounds__(kWave * kChainWaves) void emb_heavy_chain_kernel(const float* __restrict__ parts,
+                                                                             int64_t D,
+                                                                             const int32_t* __restrict__ row_lo,
+                                                                             const int32_t* __restrict__ heavy_list,
+                                                                             const int32_t* __restrict__ heavy_base,
+                                                                             const int32_t* __restrict__ long_list,
+                                                                             const int32_t* __restrict__ long_base,
+                                                                             const int* __restrict__ counts,
+                                                                             float scale, int scale_mode,
+                                                                             uint16_t* __restrict__ out) {
+    __shared__ float buf[kChainRows][kWave];
+    const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+    const int64_t ncg = (D + kWave - 1) / kWave;
+    const int64_t long_items = (int64_t)counts[2] * ncg;
+    for (int64_t item = blockIdx.x; item < long_items; item += gridDim.x) {
+        const int h = (int)(item / ncg);
+        const int64_t col = (item % ncg) * kWave + lane;
+        const bool valid = col < D;
+        const int64_t t = long_list[h];
+        const int64_t nrun = (row_lo[t + 1] - row_lo[t] + kRowsPerPartial - 1) / kRowsPerPartial;
+        const float* src = parts + (int64_t)long_base[h] * D + col;
+        float acc = 0.0f;
+        for (int64_t b = 0; b < nrun; b += kChainRows) {
+            float x[kChainDepth];
+#pragma unroll
+            for (int i = 0; i < kChainDepth; ++i) {
+                const int64_t k = b + wave + (int64_t)kChainWaves * i;
+                x[i] = (k < nrun && valid) ? src[k * D] : 0.0f;
+            }
+#pragma unroll
+            for (int i = 0; i < kChainDepth; ++i) buf[wave + kChainWaves * i][lane] = x[i];
             __syncthreads();
-            if (wave == 0) {
-                for (int w = 0; w < kHeavyWaves; ++w) {
-                    if (b + w < nrun) {
+            if (wave == 0) {                                   // LDS reads issued 16 at a time, added in order
+                const int n = (int)(nrun - b < kChainRows ? nrun - b : kChainRows);
+                for (int k0 = 0; k0 < n; k0 += 16) {
+                    float y[16];
 #pragma unroll
-                        for (int k = 0; k < kCols; ++k) acc[k] = acc[k] + parts[w][lane][k];
-                    }
+                    for (int i = 0; i < 16; ++i) y[i] = buf[k0 + i][lane];
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (k0 + i < n) acc = acc + y[i];
                 }
             }
             __syncthreads();
         }
-        if (wave == 0 && valid) {
-            uint16_t* orow = out + t * D + c0;
-            if (VEC) {
-                u4 o;
+        if (wave == 0 && valid) out[t * D + col] = finish(acc, scale, scale_mode);
+    }
+    const int64_t items = (int64_t)counts[0] * ncg;
+    for (int64_t item = (int64_t)blockIdx.x * kChainWaves + wave; item < items;
+         item += (int64_t)gridDim.x * kChainWaves) {
+        const int h = (int)(item / ncg);
+        const int64_t col = (item % ncg) * kWave + lane;
+        if (col >= D) continue;
+        const int64_t t = heavy_list[h];
+        const int nrun = (int)((row_lo[t + 1] - row_lo[t] + kRowsPerPartial - 1) / kRowsPerPartial);
+        const float* src = parts + (int64_t)heavy_base[h] * D + col;
+        float x[kWaveChainRuns];
 #pragma unroll
-                for (int k = 0; k < 8; k += 2)
-                    o[k >> 1] = (uint32_t)finish(acc[k], scale, scale_mode) |
-                                ((uint32_t)finish(acc[k + 1], scale, scale_mode) << 16);
-                nt_store(reinterpret_cast<u4*>(orow), o);
-            } else {
-                orow[0] = finish(acc[0], scale, scale_mode);
-            }
-        }
+        for (int k = 0; k < kWaveChainRuns; ++k) x[k] = k < nrun ? src[(int64_t)k * D] : 0.0f;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < kWaveChainRuns; ++k)
+            if (k < nrun) acc = acc + x[k];
+        out[t * D + col] = finish(acc, scale, scale_mode);
     }
 }
 
@@ -274,54 +349,88 @@ size_t sort_temp_bytes(int64_t R) {
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+// Workspace: keys, positions, sorted keys, sorted positions (R each), row_lo (V + 1), the three counters, the two
+// lists of heavy tokens and their first run slots (at most R / 21 each), the run starts and the fp32 partials (R / 7
+// slots, D each), then the sort's temporary storage.
+struct EmbWorkspace {
+    uint32_t* keys;
+    int32_t* vals;
+    uint32_t* skeys;
+    int32_t* svals;
+    int32_t* row_lo;
+    int* counts;
+    int32_t* heavy_list;
+    int32_t* heavy_base;
+    int32_t* long_list;
+    int32_t* long_base;
+    int32_t* run_start;
+    float* parts;
+    void* temp;
+    size_t temp_bytes;
+    size_t total;
+};
+
+EmbWorkspace emb_workspace(void* base, int64_t R, int64_t D, int64_t V) {
+    EmbWorkspace w{};
+    unsigned char* p = static_cast<unsigned char*>(base);
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        unsigned char* q = p ? p + off : nullptr;
+        off += align256(bytes > 0 ? bytes : 1);
+        return q;
+    };
+    const size_t r = (size_t)R, heavy = (size_t)(R / (kHeavyRows + 1)), slots = (size_t)(R / 7);
+    w.keys = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * r));
+    w.vals = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * r));
+    w.skeys = reinterpret_cast<uint32_t*>(take(sizeof(uint32_t) * r));
+    w.svals = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * r));
+    w.row_lo = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * (size_t)(V + 1)));
+    w.counts = reinterpret_cast<int*>(take(3 * sizeof(int)));
+    w.heavy_list = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * heavy));
+    w.heavy_base = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * heavy));
+    w.long_list = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * heavy));
+    w.long_base = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * heavy));
+    w.run_start = reinterpret_cast<int32_t*>(take(sizeof(int32_t) * slots));
+    w.parts = reinterpret_cast<float*>(take(sizeof(float) * slots * (size_t)D));
+    w.temp_bytes = sort_temp_bytes(R);
+    w.temp = take(w.temp_bytes);
+    w.total = off;
+    return w;
+}
+
 }  // namespace
 
 extern "C" {
 
-// Workspace: keys, positions, sorted keys, sorted positions (R each), row_lo (V + 1), the heavy-token count and
-// list (V), then the sort's temporary storage.
-int64_t z1_embedding_backward_workspace(int64_t R, int64_t V) {
-    if (R < 0 || R > INT32_MAX || V <= 0 || V > INT32_MAX - 1) return Z1_E_SIZE;
-    const size_t kb = align256(sizeof(uint32_t) * (size_t)(R > 0 ? R : 1));
-    return (int64_t)(4 * kb + align256(sizeof(int32_t) * (size_t)(V + 1)) + 256 +
-                     align256(sizeof(int32_t) * (size_t)V) + align256(sort_temp_bytes(R)));
+int64_t z1_embedding_backward_workspace(int64_t R, int64_t D, int64_t V) {
+    if (R < 0 || R > INT32_MAX || D <= 0 || D > kMaxCols || V <= 0 || V > INT32_MAX - 1) return Z1_E_SIZE;
+    return (int64_t)emb_workspace(nullptr, R, D, V).total;
 }
 
 int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, int64_t D, int64_t V,
                           int64_t padding_idx, float scale, int scale_mode, uint16_t* out, void* workspace,
                           int64_t workspace_bytes, void* stream) {
     if (!out || !workspace || (R > 0 && (!ids || !grad))) return Z1_E_NULL;
-    if (R < 0 || R > INT32_MAX || D <= 0 || V <= 0 || V > INT32_MAX - 1) return Z1_E_SIZE;
     if (scale_mode < 0 || scale_mode > 2) return Z1_E_MODE;
-    const int64_t need = z1_embedding_backward_workspace(R, V);
+    const int64_t need = z1_embedding_backward_workspace(R, D, V);
     if (need < 0) return (int)need;
     if (workspace_bytes < need) return Z1_E_WORKSPACE;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    const size_t kb = align256(sizeof(uint32_t) * (size_t)(R > 0 ? R : 1));
-    unsigned char* w = static_cast<unsigned char*>(workspace);
-    uint32_t* keys = reinterpret_cast<uint32_t*>(w);
-    int32_t* vals = reinterpret_cast<int32_t*>(w + kb);
-    uint32_t* skeys = reinterpret_cast<uint32_t*>(w + 2 * kb);
-    int32_t* svals = reinterpret_cast<int32_t*>(w + 3 * kb);
-    int32_t* row_lo = reinterpret_cast<int32_t*>(w + 4 * kb);
-    const size_t rl = align256(sizeof(int32_t) * (size_t)(V + 1));
-    int* heavy_count = reinterpret_cast<int*>(w + 4 * kb + rl);
-    int32_t* heavy_list = reinterpret_cast<int32_t*>(w + 4 * kb + rl + 256);
-    void* temp = w + 4 * kb + rl + 256 + align256(sizeof(int32_t) * (size_t)V);
+    const EmbWorkspace w = emb_workspace(workspace, R, D, V);
     hipError_t e = hipSuccess;
     if (R > 0) {
-        hipLaunchKernelGGL(emb_keys_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, ids, R, V, keys,
-                           vals);
+        hipLaunchKernelGGL(emb_keys_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, st, ids, R, V, w.keys,
+                           w.vals);
         e = hipGetLastError();
         if (e != hipSuccess) return (int)e;
-        size_t tb = sort_temp_bytes(R);
+        size_t tb = w.temp_bytes;
         int end_bit = 1;
         while (end_bit < 32 && ((uint64_t)V >> end_bit) != 0) ++end_bit;   // keys are <= V
-        e = hipcub::DeviceRadixSort::SortPairs(temp, tb, keys, skeys, vals, svals, (int)R, 0, end_bit, st);
+        e = hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.keys, w.skeys, w.vals, w.svals, (int)R, 0, end_bit, st);
         if (e != hipSuccess) return (int)e;
     }
-    hipLaunchKernelGGL(emb_row_ranges_kernel, dim3((unsigned)((V + 1 + 255) / 256)), dim3(256), 0, st, skeys, R, V,
-                       row_lo, heavy_count);
+    hipLaunchKernelGGL(emb_row_ranges_kernel, dim3((unsigned)((V + 1 + 255) / 256)), dim3(256), 0, st, w.skeys, R, V,
+                       w.row_lo, w.counts);
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     const int vec = (D % 8 == 0) && ((reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(out)) & 15) == 0;
@@ -331,16 +440,22 @@ int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, i
     size_t lds = 0;
     const int rc = z1detail::occupancy_lds(dev, kEmbWgPerCu, &lds);
     if (rc) return rc;
-    hipLaunchKernelGGL(emb_rows_kernel, dim3((unsigned)V), dim3(kEmbThreads), lds, st, grad, D, svals, row_lo,
-                       padding_idx, scale, scale_mode, vec, out, heavy_count, heavy_list);
+    hipLaunchKernelGGL(emb_rows_kernel, dim3((unsigned)V), dim3(kEmbThreads), lds, st, grad, D, w.svals, w.row_lo,
+                       padding_idx, scale, scale_mode, vec, out, w.counts, w.heavy_list, w.heavy_base, w.long_list, w.long_base,
+                       w.run_start);
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     if (vec)
-        hipLaunchKernelGGL(emb_heavy_kernel<1>, dim3(kHeavyGrid), dim3(kWave * kHeavyWaves), 0, st, grad, D, svals,
-                           row_lo, scale, scale_mode, out, heavy_count, heavy_list);
+        hipLaunchKernelGGL(emb_heavy_parts_kernel<1>, dim3(kPartsGrid), dim3(kPartsThreads), 0, st, grad, D, w.svals,
+                           w.skeys, w.row_lo, w.run_start, w.counts, scale, scale_mode, w.parts);
     else
-        hipLaunchKernelGGL(emb_heavy_kernel<0>, dim3(kHeavyGrid), dim3(kWave * kHeavyWaves), 0, st, grad, D, svals,
-                           row_lo, scale, scale_mode, out, heavy_count, heavy_list);
+        hipLaunchKernelGGL(emb_heavy_parts_kernel<0>, dim3(kPartsGrid), dim3(kPartsThreads), 0, st, grad, D, w.svals,
+                           w.skeys, w.row_lo, w.run_start, w.counts, scale, scale_mode, w.parts);
+    e = hipGetLastError();
+    if (e != hipSuccess) return (int)e;
+    hipLaunchKernelGGL(emb_heavy_chain_kernel, dim3(kChainGrid), dim3(kWave * kChainWaves), 0, st, w.parts, D,
+                       w.row_lo, w.heavy_list, w.heavy_base, w.long_list, w.long_base, w.counts, scale, scale_mode,
+                       out);
     e = hipGetLastError();
     return e == hipSuccess ? Z1_OK : (int)e;
 }

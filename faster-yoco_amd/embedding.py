@@ -13,8 +13,8 @@ from . import ops
 from ._lib import check, lib, ptr, require_gpu, stream_handle
 
 
-def workspace_bytes(rows, num_weights):
-    n = int(lib().z1_embedding_backward_workspace(int(rows), int(num_weights)))
+def workspace_bytes(rows, dim, num_weights):
+    n = int(lib().z1_embedding_backward_workspace(int(rows), int(dim), int(num_weights)))
     if n < 0:
         check(n, 'z1_embedding_backward_workspace')
     return n
@@ -43,7 +43,7 @@ def embedding_dense_backward(grad, indices, num_weights, padding_idx, scale_grad
           or out.device != g.device):
         raise RuntimeError('embedding_dense_backward: out must be a contiguous bf16 [num_weights, D] tensor')
     R = g.shape[0]
-    ws = torch.empty(workspace_bytes(R, num_weights), dtype=torch.uint8, device=g.device)
+    ws = torch.empty(workspace_bytes(R, D, num_weights), dtype=torch.uint8, device=g.device)
     mode = 0 if scale is None else (1 if scale_first else 2)
     with torch.cuda.device(g.device):
         check(lib().z1_embedding_backward(ptr(idx), ptr(g), R, D, int(num_weights), int(padding_idx),

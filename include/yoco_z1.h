@@ -146,11 +146,12 @@ int z1_cast_bf16(const float* p32, uint16_t* p16, int64_t n, void* stream);
  * rows scaled first, scale_mode 1; 0: no scale).  Same order as aten's sort-based GPU path: each id's occurrences
  * in position order, fp32 partial sums over runs of 10, partials summed in order, one bf16 rounding.  Every row of
  * out is written (rows without occurrences, padding_idx and ids outside [0, V) give zeros).  workspace: device
- * memory of z1_embedding_backward_workspace(R, V) bytes. */
+ * memory of z1_embedding_backward_workspace(R, D, V) bytes (with D <= 2^24: about 4/7 of R x D x 4 bytes for
+ * the fp32 run partials of frequent ids, and R x 16 + V x 4 bytes plus the radix sort's storage).  */
 int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, int64_t D, int64_t V,
                           int64_t padding_idx, float scale, int scale_mode, uint16_t* out, void* workspace,
                           int64_t workspace_bytes, void* stream);
-int64_t z1_embedding_backward_workspace(int64_t R, int64_t V);
+int64_t z1_embedding_backward_workspace(int64_t R, int64_t D, int64_t V);
 
 /* Text for a return code (negative: argument errors; positive: hipError_t). */
 const char* z1_strerror(int code);

@@ -16,7 +16,10 @@ int main(void) {
     z1_update_scalars u;
     memset(&u, 0, sizeof(u));
     bad |= z1_update_scalars_run(0, &u, 0) != Z1_E_NULL;
-    bad |= z1_embedding_backward_workspace(-1, 10) != Z1_E_SIZE;
+    bad |= z1_embedding_backward_workspace(-1, 8, 10) != Z1_E_SIZE;
+    bad |= z1_embedding_backward_workspace(16, 0, 10) != Z1_E_SIZE;
+    bad |= z1_embedding_backward_workspace(16, (1 << 24) + 1, 10) != Z1_E_SIZE;
+    bad |= z1_embedding_backward_workspace(16, 8, 10) <= 0;
     bad |= z1_adam_cast_dev(0, 0, 0.f, 0.f, 0.f, 0.f, 0, 0.f, 1, 0) != Z1_E_NULL;
     bad |= z1_bias_corrections_step(0, 0.9, 0.95, 1, 0, 0) != Z1_E_NULL;
     printf("%s\n", bad ? "FAIL" : "ok");

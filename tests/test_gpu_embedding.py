@@ -56,6 +56,30 @@ def test_matches_aten_at_larger_row_counts(pkg, dev, R):
     assert np.array_equal(bits(got), bits(ref))
 
 
+@pytest.mark.parametrize('D', [3072, 40, 13])
+def test_heavy_ids_at_the_run_boundaries(pkg, dev, D):
+    """Ids with 20 occurrences (the rows kernel's most), 21 (the heavy passes' fewest), 30, 31, 320 (the most one
+    wave chains: 32 runs), 321 and 9,878; 400 ids
+    with exactly 21 each, which fill every run slot the workspace holds (R / 7); one id taking every row.  Against
+    aten's sort path (more than 3072 rows in every case), on the vector path with several and with one partial
+    column group, and on the element path."""
+    from faster_yoco_amd import embedding
+    rng = np.random.default_rng(D)
+    V = 5000
+    mix = np.concatenate([np.full(c, t) for t, c in ((7, 20), (8, 21), (9, 30), (10, 31), (11, 9878), (12, 1),
+                                                     (13, 320), (14, 321))] + [rng.integers(15, V, 3000)])
+    cases = [rng.permutation(mix), rng.permutation(np.repeat(np.arange(100, 500), 21)), np.full(16384, 4)]
+    for ids in cases:
+        ids = torch.from_numpy(ids.astype(np.int64)).to(dev)
+        R = ids.numel()
+        g = (torch.randn(R, D, device=dev) * 1e-2).to(torch.bfloat16)
+        for pad in (-1, 8):
+            ref = torch.ops.aten.embedding_dense_backward(g, ids, V, pad, False)
+            got = embedding.embedding_dense_backward(g, ids, V, pad)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(got), bits(ref)), (R, pad)
+
+
 def test_matches_oracle_and_edge_cases(pkg, dev):
     from faster_yoco_amd import embedding
     rng = np.random.default_rng(3)
