@@ -199,10 +199,12 @@ def adam_cast_dev(table, factor, lr, beta1, beta2, eps, bc, weight_decay, mode):
 def bias_corrections_step(step, beta1, beta2, bc, bias_correction=1):
     """On the device: step += 1, bc = fp32(1 - beta**step) in double (yoco/tasks/fused_adam_cast.py:58-60).
     step: 1-element int64 device tensor; bc: 2-element fp32 device tensor."""
-    for t, what in ((step, 'step'), (bc, 'bc')):
+    for t in (step, bc):
         require_gpu(t, 'bias_corrections_step')
-    if step.dtype != torch.int64 or bc.dtype != torch.float32 or bc.numel() < 2:
-        raise RuntimeError('yoco_z1: bias_corrections_step takes an int64 step and a 2-element fp32 bc')
+    if (step.dtype != torch.int64 or step.numel() < 1 or bc.dtype != torch.float32 or bc.numel() < 2
+            or not bc.is_contiguous() or step.device != bc.device):
+        raise RuntimeError('yoco_z1: bias_corrections_step takes an int64 step and a contiguous 2-element fp32 bc '
+                           'on one device')
     with torch.cuda.device(step.device):
         check(lib().z1_bias_corrections_step(ptr(step), float(beta1), float(beta2), int(bias_correction), ptr(bc),
                                              stream_handle(step.device)), 'z1_bias_corrections_step')

@@ -30,7 +30,10 @@ class FlatShard:
             raise RuntimeError('yoco_z1: gradients must be fp32 or bf16')
         if align < 1 or align & (align - 1):
             raise RuntimeError('yoco_z1: align must be a power of two')
-        self.device = torch.device(device)
+        dev = torch.device(device)
+        if dev.type == 'cuda' and dev.index is None:
+            dev = torch.device('cuda', torch.cuda.current_device())
+        self.device = dev
         self.shapes = [tuple(int(d) for d in s) for s in shapes]
         self.numels = [_numel(s) for s in self.shapes]
         self.offsets = []
@@ -101,6 +104,22 @@ class Zero1ShardOptimizer:
         self._step_dev = torch.zeros(1, dtype=torch.int64, device=dev) if device_step else None
         self._bc = torch.ones(2, dtype=torch.float32, device=dev) if device_step else None
 
+    def _as_device_factor(self, t):
+        """A tensor factor as the 1-element fp32 device tensor the kernels read (the same tensor when it is one)."""
+        if t.dtype == torch.float32 and t.device == self.shard.device and t.numel() == 1:
+            return t
+        return t.to(device=self.shard.device, dtype=torch.float32).reshape(1)
+
+    def _clip_factor_args(self):
+        """(factor the clip chain reads, tensor it writes the clipped factor to): a tensor factor is updated in
+        place, as ``self._multiply_factor *= clip_coef`` on a tensor; a Python factor becomes a device tensor, as in
+        the reference (yoco/tasks/zero1_fast.py:158-160)."""
+        factor = self._multiply_factor
+        if torch.is_tensor(factor):
+            factor = self._as_device_factor(factor)
+            return factor, factor
+        return factor, self._factor
+
     # -- fairseq surface -------------------------------------------------------------------------------------
     def multiply_grads(self, c):
         """fairseq: ``self._multiply_factor *= c`` (c a number or a device tensor)."""
@@ -123,13 +142,7 @@ class Zero1ShardOptimizer:
         if not self._partials_ready:
             ops.grad_sumsq(self.shard.table, self._partials)
         self._partials_ready = False
-        factor = self._multiply_factor
-        if torch.is_tensor(factor):
-            if not (factor.dtype == torch.float32 and factor.is_cuda and factor.numel() == 1):
-                factor = factor.to(device=self.shard.device, dtype=torch.float32).reshape(1)
-            out = factor                # in place, as `self._multiply_factor *= clip_coef` on a tensor
-        else:
-            out = self._factor          # a Python factor becomes a device tensor, as in the reference
+        factor, out = self._clip_factor_args()
         grad_norm = torch.empty(1, dtype=torch.float32, device=self.shard.device)
         mn = float(max_norm)
         if aggregate_norm_fn is None:
@@ -152,13 +165,7 @@ class Zero1ShardOptimizer:
         if not self._partials_ready:
             ops.grad_sumsq(self.shard.table, self._partials)
         self._partials_ready = False
-        factor = self._multiply_factor
-        if torch.is_tensor(factor):
-            if not (factor.dtype == torch.float32 and factor.is_cuda and factor.numel() == 1):
-                factor = factor.to(device=self.shard.device, dtype=torch.float32).reshape(1)
-            out = factor
-        else:
-            out = self._factor
+        factor, out = self._clip_factor_args()
         grad_norm = torch.empty(1, dtype=torch.float32, device=self.shard.device)
         mn = float(max_norm)
         ops.update_scalars(self._partials, sample_size=sample_size, numer=numer, factor=factor,
@@ -181,8 +188,7 @@ class Zero1ShardOptimizer:
         bc1, bc2 = ops.bias_corrections(self.betas[0], self.betas[1], self.step_count, self.bias_correction)
         factor = self._multiply_factor
         if torch.is_tensor(factor):
-            if not (factor.dtype == torch.float32 and factor.is_cuda and factor.numel() == 1):
-                factor = factor.to(device=self.shard.device, dtype=torch.float32).reshape(1)
+            factor = self._as_device_factor(factor)
         elif float(factor) == 1.0:
             factor = None
         else:

@@ -60,6 +60,9 @@ typedef struct z1_table z1_table;            /* opaque, device-resident table + 
  * lane; overlapping rows race).  Replaces the per-call tensor-list walk of yoco/tasks/fused_adam_cast.py:62-72 and the bucket/view
  * bookkeeping of yoco/tasks/zero1_fast.py:110-128 with one schedule built at set-up.  Allocates (hipMalloc). */
 int z1_table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table** out);
+/* Frees a table (hipFree, which first waits for the device's queued work, so launches already enqueued with the
+ * table complete).  Not during stream capture; a captured graph whose launches use the table must not be replayed
+ * after it. */
 int z1_table_destroy(z1_table* table);
 /* Total elements and chunk count of a table (host-side values). */
 int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* nrows);
