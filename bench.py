@@ -25,6 +25,9 @@ WORKLOADS = {
     'c3': 'C3 owner reduce: 8 bf16 contributions of the C2 shard summed in rank order, fused norm, Adam on bf16 g',
     'c4': 'C4 unsharded YOCO-3B: 3,445,303,296 params in 304 fp32 tensors, step 1000',
     'c5': 'C5 C2 with Student-t(2) gradients and 0.1% +-1e4 outliers (clip active)',
+    'c2r': 'C2R rank 0 of YOCO-3B\'s 240 real tensors under the greedy 8-rank partition: 443,357,184 params in 9 '
+           'fp32 tensors (the largest shard), step 1000',
+    'c4r': 'C4R unsharded YOCO-3B on its 240 real tensors: 3,445,303,296 params, step 1000',
 }
 
 
@@ -189,19 +192,21 @@ def dropin_timing(dev, hp, step, reps=10):
 def embedding_timing(dev, reps=20):
     """The embedding owner's gradient at the recipe's size (8 ranks x 2048 token rows of 3072, vocabulary 100,288):
     torch's aten.embedding_dense_backward + x 1/world as the reference runs it, against this build's fused kernel;
-    HIP events on the current stream, milliseconds per call."""
+    HIP events on the current stream, milliseconds per call.  Uniform ids (the top-level keys) and Zipf(1.2) ids
+    (``zipf1_2``: token frequencies as in text, the most frequent id on about 18 % of the rows)."""
+    import numpy as np
     import torch
     from faster_yoco_amd import embedding
     R, D, V = 8 * 2048, 3072, 100288
     gen = torch.Generator(device=dev)
     gen.manual_seed(0)
-    ids = torch.randint(0, V, (R,), device=dev, generator=gen)
+    uniform = torch.randint(0, V, (R,), device=dev, generator=gen)
     g = (torch.randn(R, D, device=dev, generator=gen) * 1e-2).to(torch.bfloat16)
-    out = torch.empty(V, D, dtype=torch.bfloat16, device=dev)
-    res = {}
-    for name, fn in (('aten_embedding_dense_backward', lambda: torch.ops.aten.embedding_dense_backward(
-                          g, ids, V, -1, False).mul_(1.0 / 8)),
-                     ('z1_embedding_backward', lambda: embedding.owner_embedding_grad(g, ids, V, -1, 8))):
+    rng = np.random.default_rng(0)
+    z = rng.zipf(1.2, R) - 1
+    zipf = torch.from_numpy(np.where(z < V, z, rng.integers(0, V, R)).astype(np.int64)).to(dev)
+
+    def timed(fn):
         for _ in range(3):
             fn()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -211,8 +216,18 @@ def embedding_timing(dev, reps=20):
             fn()
         e1.record()
         torch.cuda.synchronize()
-        res[name] = round(e0.elapsed_time(e1) / reps, 4)
-    del out
+        return round(e0.elapsed_time(e1) / reps, 4)
+
+    res = {}
+    for key, ids in (('uniform', uniform), ('zipf1_2', zipf)):
+        r = {'aten_embedding_dense_backward': timed(lambda: torch.ops.aten.embedding_dense_backward(
+                 g, ids, V, -1, False).mul_(1.0 / 8)),
+             'z1_embedding_backward': timed(lambda: embedding.owner_embedding_grad(g, ids, V, -1, 8)),
+             'longest_run': int(torch.bincount(ids, minlength=V).max().item())}
+        if key == 'uniform':
+            res.update(r)
+        else:
+            res[key] = r
     res.update(rows=R, dim=D, vocab=V, bytes_written=V * D * 2)
     return res
 

@@ -5,6 +5,9 @@ C2  one GPU's YOCO-3B ZeRO-1 shard: 430,662,912 params in 38 tensors, step 1000
 C3  C2 fed by 8 BF16 owner-side contributions summed in rank order (fused owner sum + norm)
 C4  the unsharded YOCO-3B update: C2's list x 8 = 304 tensors, 3,445,303,296 params
 C5  C2 with heavy-tailed (Student-t nu=2) gradients and 0.1% +-1e4 outliers (clip coefficient << 1)
+C2R C2 on the real model's tensors: rank 0's shard of YOCO-3B's 240 tensors under the reference's greedy partition
+    over 8 ranks, 443,357,184 params in 9 tensors (the largest of the eight shards, so the one that paces a step)
+C4R C4 on the real model's tensors: YOCO-3B's 240 tensors, 3,445,303,296 params
 
 Inputs are synthetic.  GPU inputs come from torch's seeded generator on the device (``fill_shard``); small parity
 inputs come from NumPy's seeded PCG64 on the host (``host_inputs``) so the oracle sees the same arrays.
@@ -13,6 +16,8 @@ import math
 
 import numpy as np
 import torch
+
+from . import layout
 
 HPARAMS = dict(lr=3e-4, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1, max_norm=1.0)
 
@@ -35,12 +40,26 @@ def c4_shapes():
     return c2_shapes() * 8
 
 
+def yoco3b_shapes():
+    """YOCO-3B's 240 trainable tensors in model order."""
+    return layout.yoco3b_param_shapes()
+
+
+def yoco3b_rank_shapes(rank=0, world=8):
+    """The tensors rank `rank` owns under the greedy partition of YOCO-3B over `world` ranks, in model order."""
+    s = yoco3b_shapes()
+    owner, _ = layout.greedy_partition([math.prod(x) for x in s], world)
+    return [x for x, r in zip(s, owner) if r == rank]
+
+
 CONFIGS = {
     'c1': dict(shapes=C1_SHAPES, step=1, grad='normal', g_std=1e-3, m_std=0.0, v_std=0.0),
     'c2': dict(shapes=None, step=1000, grad='normal', g_std=1e-4, m_std=1e-4, v_std=1e-8),
     'c3': dict(shapes=None, step=1000, grad='owner8', g_std=1e-4, m_std=1e-4, v_std=1e-8),
     'c4': dict(shapes=None, step=1000, grad='normal', g_std=1e-4, m_std=1e-4, v_std=1e-8),
     'c5': dict(shapes=None, step=1000, grad='student_t', g_std=1e-3, m_std=1e-4, v_std=1e-8),
+    'c2r': dict(shapes=None, step=1000, grad='normal', g_std=1e-4, m_std=1e-4, v_std=1e-8),
+    'c4r': dict(shapes=None, step=1000, grad='normal', g_std=1e-4, m_std=1e-4, v_std=1e-8),
 }
 
 
@@ -51,6 +70,10 @@ def shapes(name):
         return c2_shapes()
     if name == 'c4':
         return c4_shapes()
+    if name == 'c2r':
+        return yoco3b_rank_shapes(0)
+    if name == 'c4r':
+        return yoco3b_shapes()
     raise KeyError(name)
 
 
@@ -173,7 +196,7 @@ def bf16_bits(t):
 # into floats that are small integers times powers of two (exact in fp32; the BF16 contributions exact in bf16).
 _M32 = 0xFFFFFFFF
 _STREAM = {'p': 1, 'm': 2, 'v': 3, 'g': 4, 'scale': 5, 'pick': 6, 'sign': 7}   # contribution r: 16 + r
-HASHED_CONFIGS = ('c2', 'c3', 'c5', 'c4')
+HASHED_CONFIGS = ('c2', 'c3', 'c5', 'c4', 'c2r', 'c4r')
 
 
 def _mix32(x):

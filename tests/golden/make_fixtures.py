@@ -102,7 +102,8 @@ PREFIX = 1 << 20                      # elements of each input whose digest is r
 
 
 def large_digest(name, chunk=1 << 25):
-    """The full-size update of config `name` (c2, c3, c5: the 430,662,912-parameter shard; c4: 3,445,303,296) on
+    """The full-size update of config `name` (c2, c3, c5: the 430,662,912-parameter shard; c2r: 443,357,184; c4,
+    c4r: 3,445,303,296) on
     the hashed inputs of configs.hashed_values, through the oracle, streamed in chunks of `chunk` elements: pass 1
     sums the squares of the gradient (c3: of the rank-order BF16 average of the eight contributions, x 1/8), the
     chunk sums added in FP64; norm -> clip at 1.0; pass 2 runs Adam mode 1 at step 1000 with the clipped factor and
@@ -149,8 +150,20 @@ def large_digest(name, chunk=1 << 25):
 
 def main():
     if '--large' in sys.argv[1:]:
-        d = {name: large_digest(name) for name in ('c2', 'c3', 'c5', 'c4')}
-        with open(os.path.join(HERE, 'large_digests.json'), 'w') as f:
+        # --large [name ...]: (re)computes the named configs (default: all) and keeps the others' entries
+        import __graft_entry__
+        __graft_entry__.package()
+        from faster_yoco_amd import configs
+        names = [a for a in sys.argv[1:] if not a.startswith('--')] or list(configs.HASHED_CONFIGS)
+        path = os.path.join(HERE, 'large_digests.json')
+        d = {}
+        if os.path.exists(path):
+            with open(path) as f:
+                d = json.load(f)
+        for name in names:
+            d[name] = large_digest(name)
+            print('large digest of', name, 'done', flush=True)
+        with open(path, 'w') as f:
             json.dump(d, f, indent=1)
             f.write('\n')
         print('large digests written to', HERE)

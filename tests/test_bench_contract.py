@@ -1,0 +1,40 @@
+"""bench.py's contract on the CPU: one GPU only (any other --gpus exits with a message before touching a device),
+one workload per configuration, and the algorithmic bytes per parameter of the two kinds of step (norm 4 + Adam 30
+with fp32 gradients; owner sum 18 + Adam 28 with bf16 ones)."""
+import json
+import os
+import subprocess
+import sys
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, ROOT)
+
+import bench  # noqa: E402
+
+
+def test_more_than_one_gpu_exits_with_a_message():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, 'bench.py'), '--gpus', '2'], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert 'one GPU only' in r.stderr and r.stdout == ''
+
+
+def test_workloads_cover_every_config(pkg):
+    from faster_yoco_amd import configs
+    assert set(bench.WORKLOADS) == set(configs.CONFIGS)
+
+
+def test_algorithmic_bytes():
+    n = 430_662_912
+    assert bench.algorithmic_bytes('c2', n) == (34 * n, 30 * n, 30)
+    assert bench.algorithmic_bytes('c3', n) == (46 * n, 28 * n, 28)
+    assert bench.algorithmic_bytes('c2r', 443_357_184) == (34 * 443_357_184, 30 * 443_357_184, 30)
+
+
+def test_committed_traffic_summaries_parse():
+    for kernel, workload in (('adam_cast', 'c2'), ('adam_cast', 'c3'), ('sumsq', 'c2'), ('owner_sum', 'c3')):
+        t = bench.load_traffic(kernel, workload)
+        assert t is None or t > 0, (kernel, workload)
+    with open(os.path.join(ROOT, 'profiles', 'adam_cast_c2_traffic.json')) as f:
+        d = json.load(f)
+    assert abs(d['hbm_bytes_per_launch'] / (30 * 430_662_912) - 1) < 0.01

@@ -1,6 +1,8 @@
 """Full-size updates bit-exact on every element: C2, C3 (owner sum of 8 BF16 contributions first) and C5 (values
 over 24 binades, 0.1% outliers) on the 430,662,912-parameter shard, and C4 (the unsharded 3,445,303,296-parameter
-update, 304 tensors, 62 GB resident), with inputs generated on the device by
+update, 304 tensors, 62 GB resident), and the same two on YOCO-3B's real tensors (C2R: rank 0's 9-tensor shard
+of 443,357,184 parameters under the 8-rank greedy partition; C4R: all 240 tensors), with inputs generated on the
+device by
 configs.hashed_values -- which NumPy computes bit for bit alike -- checked against tests/golden/large_digests.json,
 the CPU oracle's results on the same inputs (tests/golden/make_fixtures.py --large): the bits of the norm,
 grad_norm and clip factor, and sha256 of p, m, v, the BF16 copy and (C3) the BF16 average."""
@@ -30,7 +32,7 @@ def hexbits(t):
     return '0x%08x' % (int(t.reshape(-1)[0].view(torch.int32).item()) & 0xffffffff)
 
 
-@pytest.mark.parametrize('name', ['c2', 'c3', 'c5', 'c4'])
+@pytest.mark.parametrize('name', ['c2', 'c3', 'c5', 'c4', 'c2r', 'c4r'])
 def test_full_size_update_matches_oracle_digest(pkg, dev, name):
     from faster_yoco_amd import configs, shard as shard_mod
     with open(os.path.join(HERE, 'large_digests.json')) as f:
