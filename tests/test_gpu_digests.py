@@ -68,3 +68,50 @@ def test_full_size_update_matches_oracle_digest(pkg, dev, name):
     if 'avg16' in want:
         got['avg16'] = digest(sh.g)
     assert got == want
+
+
+def test_dropin_fused_adam_cast_full_size_matches_oracle_digest(pkg, dev):
+    """The drop-in surface at C2's full size: FusedAdamCast called with amp_C.multi_tensor_adam's signature, as
+    fairseq's FusedAdamV2.step calls it (yoco/tasks/fused_adam_cast.py:62-72), over the 38 C2 tensors allocated one
+    by one (the reference's per-parameter layout) with BF16 destinations in one flat buffer.  The gradients are
+    multiplied by the digest's clip factor first (fp32 products, as the reference's scale pass writes them), so
+    p, m, v and the BF16 copy must give C2's digests."""
+    import hashlib
+    import math
+    from faster_yoco_amd import configs
+    from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+    with open(os.path.join(HERE, 'large_digests.json')) as f:
+        d = json.load(f)['c2']
+    h = d['hparams']
+    factor = torch.tensor([int(d['factor_bits'], 16)], dtype=torch.int64).to(torch.int32).view(torch.float32)
+    factor = factor.to(dev)
+    shapes = configs.shapes('c2')
+    flat16 = torch.empty(d['params'], dtype=torch.bfloat16, device=dev)
+    tensors = {f: [] for f in ('g', 'p', 'm', 'v')}
+    dest, k = {}, 0
+    for s in shapes:
+        n = math.prod(s)
+        for f in tensors:
+            t = torch.empty(n, dtype=torch.float32, device=dev)
+            for i in range(0, n, 1 << 25):
+                idx = torch.arange(k + i, k + min(n, i + (1 << 25)), dtype=torch.int64, device=dev)
+                t[i:i + idx.numel()] = configs.hashed_values('c2', f, idx)
+            tensors[f].append(t.view(s))
+        tensors['g'][-1].mul_(factor)
+        dest[tensors['p'][-1].data_ptr()] = flat16[k:k + n].view(s)
+        k += n
+    assert k == d['params']
+    fa = FusedAdamCast(dest)
+    noop = torch.zeros(1, dtype=torch.int32, device=dev)
+    fa(2048 * 32, noop, [tensors['g'], tensors['p'], tensors['m'], tensors['v']], h['lr'], h['beta1'], h['beta2'],
+       h['eps'], d['step'], 1, 1, h['weight_decay'])
+    torch.cuda.synchronize()
+    assert len(fa.cast) == len(shapes)
+    got = {}
+    for f in ('p', 'm', 'v'):
+        hs = hashlib.sha256()
+        for t in tensors[f]:
+            hs.update(t.reshape(-1).cpu().numpy().tobytes())
+        got[f] = hs.hexdigest()
+    got['p16'] = digest(flat16)
+    assert got == {key: d['sha256'][key] for key in ('p', 'm', 'v', 'p16')}
