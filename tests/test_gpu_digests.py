@@ -115,3 +115,26 @@ def test_dropin_fused_adam_cast_full_size_matches_oracle_digest(pkg, dev):
         got[f] = hs.hexdigest()
     got['p16'] = digest(flat16)
     assert got == {key: d['sha256'][key] for key in ('p', 'm', 'v', 'p16')}
+
+
+def test_dropin_ce_sum_slots_full_size_matches_oracle_digest(pkg, dev):
+    """The copy-engine path's owner sum at C3's full size through the drop-in of CEReduce._sum
+    (yoco/models/decoder/ce_reduce.py:59-74,178-183): rank 3's own contribution in OUT, the seven peers' in the
+    slot-major staging buffer (peer k < 3 in slot k, k > 3 in slot k - 1), summed in place in three phases of
+    bounds; OUT must then hold C3's BF16 average."""
+    from faster_yoco_amd import ce_reduce, configs
+    with open(os.path.join(HERE, 'large_digests.json')) as f:
+        d = json.load(f)['c3']
+    G, R, W = d['params'], 3, 8
+    S = torch.empty((W - 1) * G, dtype=torch.bfloat16, device=dev)
+    OUT = torch.empty(G, dtype=torch.bfloat16, device=dev)
+    for k in range(W):
+        dst = OUT if k == R else S[(k if k < R else k - 1) * G:(k if k < R else k - 1) * G + G]
+        for i in range(0, G, 1 << 25):
+            idx = torch.arange(i, min(G, i + (1 << 25)), dtype=torch.int64, device=dev)
+            dst[i:i + idx.numel()] = configs.hashed_values('c3', f'c{k}', idx).to(torch.bfloat16)
+    assert digest(OUT[:d['prefix_elements']]) == d['input_prefix_sha256'][f'c{R}']
+    for a, b in ((0, 123_456_789), (123_456_789, 123_456_789), (123_456_789, G)):
+        ce_reduce.sum_slots(S, OUT, G, a, b, R, 1.0 / W, W)
+    torch.cuda.synchronize()
+    assert digest(OUT) == d['sha256']['avg16']
