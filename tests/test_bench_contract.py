@@ -38,3 +38,16 @@ def test_committed_traffic_summaries_parse():
     with open(os.path.join(ROOT, 'profiles', 'adam_cast_c2_traffic.json')) as f:
         d = json.load(f)
     assert abs(d['hbm_bytes_per_launch'] / (30 * 430_662_912) - 1) < 0.01
+
+
+def test_config_sizes(pkg):
+    """Parameter and tensor counts of every workload: C2 = C4 / 8; C2R is the largest owner of YOCO-3B's greedy
+    8-rank partition; C4R is the whole 240-tensor model."""
+    from faster_yoco_amd import configs, layout
+    import math
+    want = {'c1': (9_438_208, 4), 'c2': (430_662_912, 38), 'c3': (430_662_912, 38), 'c5': (430_662_912, 38),
+            'c4': (3_445_303_296, 304), 'c2r': (443_357_184, 9), 'c4r': (3_445_303_296, 240)}
+    for name, (n, t) in want.items():
+        assert (configs.numel(name), len(configs.shapes(name))) == (n, t), name
+    _, sizes = layout.greedy_partition([math.prod(s) for s in configs.shapes('c4r')], 8)
+    assert max(sizes) == configs.numel('c2r') and sizes.index(max(sizes)) == 0
