@@ -661,7 +661,7 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     int has_pmv = 1;
     for (int i = 0; i < nrows; ++i) {
         const z1_tensor& t = rows[i];
-        if (t.n < 0) return Z1_E_SIZE;
+        if (t.n < 0 || t.n > (int64_t)INT32_MAX * kChunk) return Z1_E_SIZE;   // also keeps the sums below in range
         if (t.n == 0) continue;
         if (!t.g) return Z1_E_NULL;
         Row r;
@@ -682,6 +682,7 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
         if (!t.p || !t.m || !t.v) has_pmv = 0;
         chunks += (t.n + kChunk - 1) / kChunk;
         numel += t.n;
+        if (chunks > INT32_MAX) return Z1_E_SIZE;
         h.push_back(r);
     }
     if (chunks > INT32_MAX) return Z1_E_SIZE;          // one workgroup per chunk: grid.x limit
