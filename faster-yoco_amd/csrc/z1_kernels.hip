@@ -850,7 +850,7 @@ int z1_bias_corrections_step(int64_t* step, double beta1, double beta2, int bias
 
 int64_t z1_owner_sum_workspace(int64_t n) {
     if (n < 0) return Z1_E_SIZE;
-    return Z1_NORM_PARTIALS + (n + kSumChunk - 1) / kSumChunk;
+    return Z1_NORM_PARTIALS + n / kSumChunk + (n % kSumChunk != 0);
 }
 
 int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
@@ -867,7 +867,7 @@ int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, floa
         srcs.p[k] = contrib[k];
         if (!aligned(contrib[k], 16)) vec = 0;
     }
-    const int64_t nchunks = (n + kSumChunk - 1) / kSumChunk;
+    const int64_t nchunks = n / kSumChunk + (n % kSumChunk != 0);
     if (nchunks > INT32_MAX) return Z1_E_SIZE;
     hipStream_t st = static_cast<hipStream_t>(stream);
     double* wave_partials = sumsq_partials ? sumsq_partials + Z1_NORM_PARTIALS : nullptr;
@@ -899,7 +899,7 @@ int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n,
     int dev = 0, grid = 0;
     int rc = current_device(&dev);
     if (rc) return rc;
-    rc = stream_grid(dev, (n + 7) / 8, &grid);
+    rc = stream_grid(dev, n / 8 + (n % 8 != 0), &grid);
     if (rc) return rc;
     const int vec = aligned(g16, 16) && aligned(g32, 16);
     hipLaunchKernelGGL(scale_up_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), g16, g32,
@@ -914,7 +914,7 @@ int z1_cast_bf16(const float* p32, uint16_t* p16, int64_t n, void* stream) {
     int dev = 0, grid = 0;
     int rc = current_device(&dev);
     if (rc) return rc;
-    rc = stream_grid(dev, (n + 7) / 8, &grid);
+    rc = stream_grid(dev, n / 8 + (n % 8 != 0), &grid);
     if (rc) return rc;
     const int vec = aligned(p32, 16) && aligned(p16, 16);
     hipLaunchKernelGGL(cast_bf16_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p32, p16, n,
