@@ -9,6 +9,7 @@ Prints ONE JSON line: ms per step (the metric), the Adam kernel's roofline from 
 launch stream, and the PyTorch-CPU restatement's time on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--config c2] [--cpu-sample-tensors T] [--no-cpu-baseline] [--dropin]
+                    [--pipeline K]
 """
 import argparse
 import json
@@ -189,6 +190,44 @@ def dropin_timing(dev, hp, step, reps=10):
     return out
 
 
+def pipeline_timing(shard, opt, k, reps=10):
+    """Adam in k row ranges of the shard with each finished range's BF16 rows copied out on a second stream
+    (faster_yoco_amd.exchange: the exchange the reference runs after the whole step, yoco/tasks/zero1_fast.py:224-226,
+    with a copy into a local buffer standing in for a peer's) against one launch and a copy after it.  On one GPU
+    the copy competes with Adam for the same HBM, so this measures what splitting costs, not what overlapping with
+    xGMI would gain.  HIP events on the current stream (the last one after it waits for the side stream), ms per
+    step, steps chained."""
+    import torch
+    from faster_yoco_amd import exchange
+    pieces = exchange.even_pieces(shard.numels, k)
+    remote = torch.empty_like(shard.p16)
+
+    def send(first, last):
+        remote[first:last].copy_(shard.p16[first:last])
+
+    px = exchange.PipelinedExchange(shard, pieces, send)
+
+    def whole_then_copy():
+        opt.step()
+        remote.copy_(shard.p16)
+
+    out = {'pieces': len(pieces) - 1, 'rows_per_piece': [b - a for a, b in zip(pieces, pieces[1:])],
+           'copy_bytes': 2 * 2 * shard.total}
+    for name, fn in (('adam_whole_ms', lambda: opt.step()), ('adam_pieces_ms', lambda: opt.step(pieces=pieces)),
+                     ('adam_then_copy_ms', whole_then_copy), ('adam_pipelined_copy_ms', lambda: px.step(opt))):
+        for _ in range(2):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[name] = round(e0.elapsed_time(e1) / reps, 4)
+    return out
+
+
 def embedding_timing(dev, reps=20):
     """The embedding owner's gradient at the recipe's size (8 ranks x 2048 token rows of 3072, vocabulary 100,288):
     torch's aten.embedding_dense_backward + x 1/world as the reference runs it, against this build's fused kernel;
@@ -240,6 +279,9 @@ def main():
     ap.add_argument('--config', default='c2', choices=sorted(WORKLOADS))
     ap.add_argument('--cpu-sample-tensors', type=int, default=1000)
     ap.add_argument('--no-cpu-baseline', action='store_true')
+    ap.add_argument('--pipeline', type=int, default=0, metavar='K',
+                    help='also time Adam in K row ranges with each range\'s BF16 rows copied out on a second stream '
+                         '(the pipelined exchange; off by default for the same reason as --dropin)')
     ap.add_argument('--dropin', action='store_true',
                     help='also time FusedAdamCast over the 38 C2 tensors allocated one by one (its launches share '
                          'the Adam kernel with the timed steps, so a kernel trace of the default run stays clean)')
@@ -348,6 +390,8 @@ def main():
     }
     if args.dropin:
         out['dropin_multi_tensor_adam'] = dropin_timing(dev, hp, step0)
+    if args.pipeline > 0:
+        out['pipelined_exchange'] = pipeline_timing(shard, opt, args.pipeline)
     print(json.dumps(out), flush=True)
 
 

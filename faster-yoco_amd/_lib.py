@@ -50,6 +50,7 @@ SIGNATURES = {
     'z1_update_scalars_run': ([_P, ctypes.POINTER(Z1UpdateScalars), _P], _I),
     'z1_adam_cast': ([_P, _P, _F, _F, _F, _F, _F, _F, _F, _I, _P], _I),
     'z1_adam_cast_dev': ([_P, _P, _F, _F, _F, _F, _P, _F, _I, _P], _I),
+    'z1_adam_cast_rows': ([_P, _I, _I, _P, _F, _F, _F, _F, _F, _F, _F, _I, _P], _I),
     'z1_bias_corrections_step': ([_P, ctypes.c_double, ctypes.c_double, _I, _P, _P], _I),
     'z1_scale_up': ([_P, _P, _P, _I64, _P], _I),
     'z1_cast_bf16': ([_P, _P, _I64, _P], _I),

@@ -180,14 +180,15 @@ __device__ __forceinline__ float load_g1(const void* g, int64_t i) {
 template <int GDT, int MODE>
 __global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row* __restrict__ rows,
                                                                        const int32_t* __restrict__ chunk_row,
-                                                                       int64_t nchunks,
+                                                                       int64_t chunk_begin, int64_t chunk_end,
                                                                        const float* __restrict__ factor,
                                                                        const float* __restrict__ bc, AdamK k) {
     const int lane = threadIdx.x & (kWave - 1);
-    // last chunk first: the end of the gradient is what the norm pass read last (still in the MALL)
-    const int64_t c = nchunks - 1 - (chunk_of_block(blockIdx.x, gridDim.x) * kAdamWaves +
-                                     __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
-    if (c < 0) return;
+    // chunks [chunk_begin, chunk_end), last chunk first: the end of the gradient is what the norm pass read last
+    // (still in the MALL)
+    const int64_t c = chunk_end - 1 - (chunk_of_block(blockIdx.x, gridDim.x) * kAdamWaves +
+                                       __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
+    if (c < chunk_begin) return;
     const float f = factor ? *factor : 1.0f;
     if (bc) {                                   // bias corrections from device memory (z1_adam_cast_dev)
         k.bc1 = bc[0];
@@ -624,6 +625,7 @@ inline int launch_status() {
 struct z1_table {
     Row* rows;            // device: nrows rows, then nchunks int32 chunk -> row entries (one allocation)
     int32_t* chunk_row;
+    std::vector<int64_t> first_chunk;   // host: first chunk of each row given to z1_table_create, + the total
     int nrows;
     int g_dtype;
     int device;
@@ -657,11 +659,13 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     const uintptr_t galign = g_dtype == Z1_F32 ? 16 : 8;
     std::vector<Row> h;
     h.reserve(nrows);
+    std::vector<int64_t> first((size_t)nrows + 1);
     int64_t chunks = 0, numel = 0;
     int has_pmv = 1;
     for (int i = 0; i < nrows; ++i) {
         const z1_tensor& t = rows[i];
         if (t.n < 0 || t.n > (int64_t)INT32_MAX * kChunk) return Z1_E_SIZE;   // also keeps the sums below in range
+        first[i] = chunks;
         if (t.n == 0) continue;
         if (!t.g) return Z1_E_NULL;
         Row r;
@@ -686,6 +690,7 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
         h.push_back(r);
     }
     if (chunks > INT32_MAX) return Z1_E_SIZE;          // one workgroup per chunk: grid.x limit
+    first[nrows] = chunks;
     int dev = 0;
     int rc = current_device(&dev);
     if (rc) return rc;
@@ -706,6 +711,7 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     tb->has_pmv = has_pmv;
     tb->numel = numel;
     tb->nchunks = chunks;
+    tb->first_chunk.swap(first);
     tb->rows = nullptr;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&tb->rows), img.empty() ? 64 : img.size());
     if (e != hipSuccess) {
@@ -791,15 +797,16 @@ int z1_clip_factor(const float* norm, const float* factor_in, float factor_value
     return launch_status();
 }
 
-static int adam_launch(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
-                       float bc1, float bc2, const float* bc, float weight_decay, int mode, void* stream) {
+static int adam_launch(const z1_table* table, int64_t chunk_begin, int64_t chunk_end, const float* factor, float lr,
+                       float beta1, float beta2, float eps, float bc1, float bc2, const float* bc, float weight_decay,
+                       int mode, void* stream) {
     if (!table) return Z1_E_NULL;
     if (mode != 0 && mode != 1) return Z1_E_MODE;
     if (!table->has_pmv) return Z1_E_NULL;
     int dev = 0;
     int rc = check_table_device(table, &dev);
     if (rc) return rc;
-    if (table->nchunks == 0) return Z1_OK;
+    if (chunk_end <= chunk_begin) return Z1_OK;
     AdamK k;
     k.lr = lr;
     k.b1 = beta1;
@@ -811,13 +818,13 @@ static int adam_launch(const z1_table* table, const float* factor, float lr, flo
     k.omb1 = 1.0f - beta1;
     k.omb2 = 1.0f - beta2;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)((table->nchunks + kAdamWaves - 1) / kAdamWaves));
+    const dim3 grid((unsigned)((chunk_end - chunk_begin + kAdamWaves - 1) / kAdamWaves));
     size_t lds = 0;
     rc = occupancy_lds(dev, kAdamWgPerCu, &lds);
     if (rc) return rc;
 #define Z1_LAUNCH_ADAM(GDT, MODE)                                                                              \
     hipLaunchKernelGGL((adam_cast_kernel<GDT, MODE>), grid, dim3(kWave * kAdamWaves), lds, s, table->rows,    \
-                       table->chunk_row, table->nchunks, factor, bc, k)
+                       table->chunk_row, chunk_begin, chunk_end, factor, bc, k)
     if (table->g_dtype == Z1_F32) {
         if (mode == 1) Z1_LAUNCH_ADAM(Z1_F32, 1);
         else Z1_LAUNCH_ADAM(Z1_F32, 0);
@@ -831,13 +838,25 @@ static int adam_launch(const z1_table* table, const float* factor, float lr, flo
 
 int z1_adam_cast(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
                  float bc1, float bc2, float weight_decay, int mode, void* stream) {
-    return adam_launch(table, factor, lr, beta1, beta2, eps, bc1, bc2, nullptr, weight_decay, mode, stream);
+    if (!table) return Z1_E_NULL;
+    return adam_launch(table, 0, table->nchunks, factor, lr, beta1, beta2, eps, bc1, bc2, nullptr, weight_decay, mode,
+                       stream);
+}
+
+int z1_adam_cast_rows(const z1_table* table, int row_begin, int row_end, const float* factor, float lr, float beta1,
+                      float beta2, float eps, float bc1, float bc2, float weight_decay, int mode, void* stream) {
+    if (!table) return Z1_E_NULL;
+    const int nrows = (int)table->first_chunk.size() - 1;
+    if (row_begin < 0 || row_end < row_begin || row_end > nrows) return Z1_E_SIZE;
+    return adam_launch(table, table->first_chunk[row_begin], table->first_chunk[row_end], factor, lr, beta1, beta2,
+                       eps, bc1, bc2, nullptr, weight_decay, mode, stream);
 }
 
 int z1_adam_cast_dev(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
                      const float* bc, float weight_decay, int mode, void* stream) {
-    if (!bc) return Z1_E_NULL;
-    return adam_launch(table, factor, lr, beta1, beta2, eps, 1.0f, 1.0f, bc, weight_decay, mode, stream);
+    if (!table || !bc) return Z1_E_NULL;
+    return adam_launch(table, 0, table->nchunks, factor, lr, beta1, beta2, eps, 1.0f, 1.0f, bc, weight_decay, mode,
+                       stream);
 }
 
 int z1_bias_corrections_step(int64_t* step, double beta1, double beta2, int bias_correction, float* bc,

@@ -185,6 +185,16 @@ def adam_cast(table, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode
                                  stream_handle(table.device)), 'z1_adam_cast')
 
 
+def adam_cast_rows(table, row_begin, row_end, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode):
+    """adam_cast over the table rows [row_begin, row_end) only (indices of the rows the table was built from)."""
+    if not 0 <= int(row_begin) <= int(row_end) <= table.nrows:
+        raise RuntimeError(f'yoco_z1: rows [{row_begin}, {row_end}) outside the table\'s {table.nrows} rows')
+    with torch.cuda.device(table.device):
+        check(lib().z1_adam_cast_rows(table.handle, int(row_begin), int(row_end), _scalar(factor, 'adam_cast_rows'),
+                                      f32(lr), f32(beta1), f32(beta2), f32(eps), f32(bc1), f32(bc2),
+                                      f32(weight_decay), int(mode), stream_handle(table.device)), 'z1_adam_cast_rows')
+
+
 def adam_cast_dev(table, factor, lr, beta1, beta2, eps, bc, weight_decay, mode):
     """adam_cast with the bias corrections read from bc (2-element fp32 device tensor) when the kernel runs."""
     require_gpu(bc, 'adam_cast_dev')

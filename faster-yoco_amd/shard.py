@@ -60,6 +60,14 @@ class FlatShard:
                          None if self.p16 is None else self.p16[sl], n))
         return rows
 
+    def row_elements(self, row_begin, row_end):
+        """[first, last) positions in the flat buffers spanned by the tensors row_begin .. row_end - 1."""
+        if not 0 <= row_begin <= row_end <= len(self.numels):
+            raise RuntimeError(f'yoco_z1: rows [{row_begin}, {row_end}) outside the shard')
+        if row_begin == row_end:
+            return 0, 0
+        return self.offsets[row_begin], self.offsets[row_end - 1] + self.numels[row_end - 1]
+
     def views(self, buf):
         """Per-tensor views of one flat buffer (``'p'``, ``'m'``, ``'v'``, ``'g'`` or ``'p16'``)."""
         b = getattr(self, buf)
@@ -182,8 +190,19 @@ class Zero1ShardOptimizer:
         if self.device_step:
             self._step_dev.fill_(int(n))
 
-    def step(self, closure=None, groups=None):
-        """Adam + BF16 over the shard with the gradient factor folded into the gradient load, then factor := 1."""
+    def step(self, closure=None, groups=None, pieces=None, on_piece=None):
+        """Adam + BF16 over the shard with the gradient factor folded into the gradient load, then factor := 1.
+
+        pieces (optional): row boundaries [0, r1, ..., nrows]; Adam then runs as one launch per range (the same
+        results), and on_piece(row_begin, row_end) is called after each range's launch is enqueued -- e.g. to record
+        an event and start sending the finished BF16 rows on another stream, the exchange the reference runs after
+        the whole step (yoco/tasks/zero1_fast.py:224-226)."""
+        if pieces is not None:              # checked before anything changes
+            if self.device_step:
+                raise RuntimeError('yoco_z1: a step in pieces takes host-rounded bias corrections (device_step=False)')
+            nrows = len(self.shard.numels)
+            if list(pieces[:1]) != [0] or pieces[-1] != nrows or any(a > b for a, b in zip(pieces, pieces[1:])):
+                raise RuntimeError(f'yoco_z1: pieces must run from 0 to {nrows} in order')
         self.step_count += 1
         bc1, bc2 = ops.bias_corrections(self.betas[0], self.betas[1], self.step_count, self.bias_correction)
         factor = self._multiply_factor
@@ -194,7 +213,13 @@ class Zero1ShardOptimizer:
         else:
             self._factor.fill_(float(factor))
             factor = self._factor
-        if self.device_step:
+        if pieces is not None:
+            for a, b in zip(pieces, pieces[1:]):
+                ops.adam_cast_rows(self.shard.table, a, b, factor, self.lr, self.betas[0], self.betas[1], self.eps,
+                                   bc1, bc2, self.weight_decay, self.mode)
+                if on_piece is not None:
+                    on_piece(a, b)
+        elif self.device_step:
             ops.bias_corrections_step(self._step_dev, self.betas[0], self.betas[1], self._bc, self.bias_correction)
             ops.adam_cast_dev(self.shard.table, factor, self.lr, self.betas[0], self.betas[1], self.eps, self._bc,
                               self.weight_decay, self.mode)

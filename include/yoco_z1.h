@@ -130,6 +130,15 @@ int z1_adam_cast(const z1_table* table, const float* factor, float lr, float bet
 int z1_adam_cast_dev(const z1_table* table, const float* factor, float lr, float beta1, float beta2, float eps,
                      const float* bc, float weight_decay, int mode, void* stream);
 
+/* z1_adam_cast over the rows [row_begin, row_end) of the table only -- indices into the rows array given to
+ * z1_table_create, empty rows included (Z1_E_SIZE outside 0 <= row_begin <= row_end <= nrows).  Same kernel and
+ * per-element arithmetic, so consecutive ranges that cover the table equal one z1_adam_cast.  For a caller that
+ * pipelines the step with the exchange of the finished BF16 rows, which the reference all-gathers after the whole
+ * step (yoco/tasks/zero1_fast.py:224-226): after each range it can record an event and start sending that range on
+ * another stream. */
+int z1_adam_cast_rows(const z1_table* table, int row_begin, int row_end, const float* factor, float lr, float beta1,
+                      float beta2, float eps, float bc1, float bc2, float weight_decay, int mode, void* stream);
+
 /* The step counter and bias corrections on the device, for z1_adam_cast_dev: ++*step, then
  * bc[0] = fp32(1 - pow(beta1, *step)), bc[1] = fp32(1 - pow(beta2, *step)) in double (bias_correction != 1:
  * 1, 1) -- yoco/tasks/fused_adam_cast.py:58-60 with FusedAdamV2's group['step'] += 1, on the device.  step: device

@@ -36,6 +36,7 @@ int main(void) {
     bad |= z1_embedding_backward_workspace(16, (1 << 24) + 1, 10) != Z1_E_SIZE;
     bad |= z1_embedding_backward_workspace(16, 8, 10) <= 0;
     bad |= z1_adam_cast_dev(0, 0, 0.f, 0.f, 0.f, 0.f, 0, 0.f, 1, 0) != Z1_E_NULL;
+    bad |= z1_adam_cast_rows(0, 0, 1, 0, 0.f, 0.f, 0.f, 0.f, 1.f, 1.f, 0.f, 1, 0) != Z1_E_NULL;
     bad |= z1_bias_corrections_step(0, 0.9, 0.95, 1, 0, 0) != Z1_E_NULL;
     printf("%s\n", bad ? "FAIL" : "ok");
     return bad;
