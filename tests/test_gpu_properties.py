@@ -32,8 +32,10 @@ def place(arr, off, dev, bf16=False):
        offs=st.lists(st.integers(0, 7), min_size=5, max_size=5),
        g_bf16=st.booleans(), with_p16=st.booleans(), mode=st.sampled_from([0, 1]),
        factor=st.one_of(st.none(), st.floats(1e-8, 4.0)), step=st.integers(1, 3000),
-       seed=st.integers(0, 2 ** 31 - 1))
-def test_adam_random_tables(pkg, dev, sizes, offs, g_bf16, with_p16, mode, factor, step, seed):
+       cuts=st.lists(st.integers(0, 8), max_size=4), seed=st.integers(0, 2 ** 31 - 1))
+def test_adam_random_tables(pkg, dev, sizes, offs, g_bf16, with_p16, mode, factor, step, cuts, seed):
+    """Adam + BF16 over a random table against the oracle; with `cuts`, as one z1_adam_cast_rows launch per range
+    between the cut rows."""
     from faster_yoco_amd import ops
     rng = np.random.default_rng(seed)
     hp = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
@@ -53,7 +55,13 @@ def test_adam_random_tables(pkg, dev, sizes, offs, g_bf16, with_p16, mode, facto
     table = ops.Table(rows, dev)
     bc1, bc2 = ops.bias_corrections(hp['beta1'], hp['beta2'], step)
     f = None if factor is None else torch.tensor([factor], dtype=torch.float32, device=dev)
-    ops.adam_cast(table, f, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2, hp['weight_decay'], mode)
+    if cuts:
+        bounds = sorted({0, len(sizes)} | {c for c in cuts if c <= len(sizes)})
+        for a, b in zip(bounds, bounds[1:]):
+            ops.adam_cast_rows(table, a, b, f, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2,
+                               hp['weight_decay'], mode)
+    else:
+        ops.adam_cast(table, f, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2, hp['weight_decay'], mode)
     torch.cuda.synchronize()
     for (pt, mt, vt, p16), (po, mo, vo, p16o) in zip(keep, ref):
         assert np.array_equal(pt.cpu().numpy().view(np.uint32), po.view(np.uint32))
