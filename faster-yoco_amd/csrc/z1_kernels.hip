@@ -12,7 +12,9 @@
 //     shard): 2.05 ms on typical boxes, against 2.52 ms for a persistent grid with a static partition (tail
 //     imbalance across CUs/XCDs) and 2.19 ms for 1024-element workgroups; the same kernel with its arithmetic
 //     replaced by additions runs at the same speed, i.e. it is at the bandwidth this 4-read / 4-write stream
-//     pattern reaches.
+//     pattern reaches.  A launch covers a chunk range: the whole table, or the chunks of a range of rows
+//     (z1_adam_cast_rows), so a step can be cut into launches whose finished rows are sent while the rest runs
+//     (2 or 4 ranges of C2 cost nothing measurable, 8 cost 13 us).
 //   * Each lane moves one 128-bit group per fp32 array (and 64 bits of bf16); a wave instruction covers 1 KiB
 //     (fp32) or 512 B (bf16) of contiguous bytes, with nontemporal hints (streams far larger than L2 and MALL).
 //     The last, partial chunk of a row (and rows whose pointers are not aligned for the vector path) run an
