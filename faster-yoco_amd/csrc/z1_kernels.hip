@@ -27,7 +27,7 @@
 //     wave per chunk with hardware dispatch (0.40 ms), 4-chunk workgroups with hardware dispatch (0.34 ms),
 //     2-8 loads in flight per wave (0.28-0.31 ms) and fewer waves (0.35-0.59 ms) were all slower.
 //   * MALL reuse between passes: the pass before Adam (the norm, or the owner sum that writes the BF16 average)
-//     touches the last kMallKeepBytes of the gradient with ordinary, allocating accesses, and Adam walks the
+//     touches the last 256 (224) MB of the gradient with ordinary, allocating accesses, and Adam walks the
 //     chunks from the last one, so its first gradient reads hit the 256 MB MALL (measured 2.05 vs 2.10 ms for
 //     Adam on the C2 shard; 128-512 MB kept, or everything, measured the same or slower).
 //   * No atomics anywhere; nothing but vector memory instructions write memory.
@@ -59,10 +59,13 @@ constexpr int kAdamWaves = 1;                                 // chunks (one per
 constexpr int kVec = 4;                                       // fp32 lanes of one 128-bit access
 constexpr int kGroups = 1;                                    // 128-bit groups per lane per array and chunk
 constexpr int64_t kChunk = (int64_t)kWave * kVec * kGroups;   // elements per chunk: one wave's share
-// The norm pass reads (the owner sum writes) the last kMallKeepBytes of the gradient with ordinary, allocating
-// accesses, so that they are still in the 256 MB MALL when the Adam pass -- which walks the chunks from the end --
-// reads them again.
+// The norm pass reads the last kMallKeepBytes of the gradient (the owner sum writes the last kOwnerSumKeepBytes of
+// the average) with ordinary, allocating accesses, so that they are still in the 256 MB MALL when the Adam pass --
+// which walks the chunks from the end -- reads them again.  Measured on C2 / C3: the norm keeps 256 MB (192-272 MB
+// no better); the owner sum 224 MB (C3 3.231-3.234 ms against 3.240-3.244 at 256 MB; 208-216 MB in between,
+// 232-240 MB slower), its allocating stores costing more than the norm's allocating loads.
 constexpr int64_t kMallKeepBytes = 256ll << 20;
+constexpr int64_t kOwnerSumKeepBytes = 224ll << 20;
 constexpr int kAdamWgPerCu = 16;                              // resident Adam workgroups per CU (occupancy_lds)
 constexpr int kOwnerSumWgPerCu = 11;                          // resident owner-sum workgroups per CU
 constexpr int kMaxDevices = 64;
@@ -893,7 +896,7 @@ int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, floa
     hipStream_t st = static_cast<hipStream_t>(stream);
     double* wave_partials = sumsq_partials ? sumsq_partials + Z1_NORM_PARTIALS : nullptr;
     if (nchunks > 0) {
-        const int64_t keep = kMallKeepBytes / (kSumChunk * (int64_t)sizeof(uint16_t));
+        const int64_t keep = kOwnerSumKeepBytes / (kSumChunk * (int64_t)sizeof(uint16_t));
         const int64_t keep_from = nchunks > keep ? nchunks - keep : 0;
         int dev = 0;
         size_t lds = 0;
