@@ -2,10 +2,11 @@
 //
 // Replaces torch.ops.aten.embedding_dense_backward(g_all, ids, V, padding_idx, False) on the embedding's owner,
 // followed or preceded by the x 1/world of the reference (yoco/models/decoder/layer_graphs.py:87-93,
-// yoco/models/decoder/ce_reduce.py:226-231).  Same summation order as aten's sort-based GPU path (which aten takes
-// for more than 3072 indices): occurrences of each token id in stable position order, fp32 partial sums over
-// runs of 10 consecutive occurrences, the partials summed in order, one rounding to bf16; padding_idx rows and
-// ids outside [0, V) contribute nothing.
+// yoco/models/decoder/ce_reduce.py:226-231).  Same summation order as aten for the row count.  For more than 3072
+// indices aten sorts: occurrences of each token id in stable position order, fp32 partial sums over runs of 10
+// consecutive occurrences, the partials summed in order, one rounding to bf16.  For fewer its other kernel walks
+// the indices in chunks of 16: per chunk and id an fp32 sum in position order, rounded to bf16 and added to the
+// bf16 row (emb_rows_kernel<true>; no heavy passes).  padding_idx rows and ids outside [0, V) contribute nothing.
 //
 //   1. keys[i] = id_i (or V when out of range), vals[i] = i;  2. stable radix sort (hipCUB / rocPRIM);
 //   3. row_lo[t] = start of id t's run in the sorted keys (one binary search per t, all in parallel);
@@ -32,6 +33,10 @@ namespace {
 
 constexpr int kEmbThreads = 64;                  // one wave per output row
 constexpr int kRowsPerPartial = 10;        // aten's NROWS_PER_THREAD
+// aten sorts for more than kSortMinRows - 1 indices; for fewer its kernel walks the indices in chunks of
+// kFewRowsChunk (torch's ROCm build; checked bit for bit against it on MI355X)
+constexpr int64_t kSortMinRows = 3073;
+constexpr int kFewRowsChunk = 16;
 // resident row workgroups per CU, capped with a dynamic LDS reservation the kernel does not use: 0.131 ms per call
 // at 9-10 per CU against 0.148 ms at the 32 the waves allow (0.144 at 16, 0.136 at 8, 0.146 at 7, 0.180 at 6)
 constexpr int kEmbWgPerCu = 10;
@@ -116,6 +121,7 @@ __device__ __forceinline__ void nt_store(u4* p, u4 x) {
 // most kWaveChainRuns runs (heavy_list / heavy_base, count counts[0]) or to that of longer ones (long_list /
 // long_base, counts[2]); run_start[slot] = the sorted position of the run's first row.  Its row is left to the heavy
 // passes.  The atomics only decide where a token's partials are kept, not how they are summed.
+template <bool FEW>
 __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* __restrict__ grad, int64_t D,
                                                                const int32_t* __restrict__ spos,
                                                                const int32_t* __restrict__ row_lo,
@@ -139,7 +145,8 @@ __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* _
     uint16_t* orow = out + t * D;
     const int64_t lo = row_lo[t], hi = row_lo[t + 1];
     const bool empty = lo == hi || t == padding_idx;
-    if (!empty && hi - lo > kHeavyRows) {
+    constexpr int chunk = kFewRowsChunk;
+    if (!FEW && !empty && hi - lo > kHeavyRows) {
         const int nrun = (int)((hi - lo + kRowsPerPartial - 1) / kRowsPerPartial);
         int base = 0;
         if (lane == 0) {
@@ -157,7 +164,43 @@ __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* _
         const int64_t ng = D / 8;
         for (int64_t gi = lane; gi < ng; gi += kEmbThreads) {
             u4 o = u4{0u, 0u, 0u, 0u};
-            if (!empty) {
+            if constexpr (FEW) {
+              if (!empty) {
+                // aten's few-indices order: the id's occurrences grouped by index chunk (positions ascend), each
+                // group's fp32 sum rounded to bf16 and added to the bf16 row
+                float acc[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) acc[k] = 0.0f;
+                for (int64_t j0 = lo; j0 < hi;) {
+                    const int32_t cid = spos[j0] / chunk;
+                    int cnt = 1;
+                    while (cnt < kFewRowsChunk && j0 + cnt < hi && spos[j0 + cnt] / chunk == cid) ++cnt;
+                    u4 x[kFewRowsChunk];
+#pragma unroll
+                    for (int u = 0; u < kFewRowsChunk; ++u)
+                        if (u < cnt) x[u] = reinterpret_cast<const u4*>(grad + (int64_t)spos[j0 + u] * D)[gi];
+                    float part[8];
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) part[k] = 0.0f;
+#pragma unroll
+                    for (int u = 0; u < kFewRowsChunk; ++u) {
+                        if (u < cnt) {
+#pragma unroll
+                            for (int k = 0; k < 8; ++k)
+                                part[k] = part[k] + grad_elem((uint16_t)(x[u][k >> 1] >> ((k & 1) * 16)), scale,
+                                                              scale_mode);
+                        }
+                    }
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) acc[k] = bf16f(bf16r(acc[k] + bf16f(bf16r(part[k]))));
+                    j0 += cnt;
+                }
+#pragma unroll
+                for (int k = 0; k < 8; k += 2)
+                    o[k >> 1] = (uint32_t)finish(acc[k], scale, scale_mode) |
+                                ((uint32_t)finish(acc[k + 1], scale, scale_mode) << 16);
+              }
+            } else if (!empty) {
                 float acc[8];
 #pragma unroll
                 for (int k = 0; k < 8; ++k) acc[k] = 0.0f;
@@ -194,7 +237,19 @@ __global__ __launch_bounds__(kEmbThreads) void emb_rows_kernel(const uint16_t* _
     }
     for (int64_t d = lane; d < D; d += kEmbThreads) {
         uint16_t o = 0;
-        if (!empty) {
+        if (FEW && !empty) {
+            float acc = 0.0f;
+            for (int64_t j0 = lo; j0 < hi;) {
+                const int32_t cid = spos[j0] / chunk;
+                float part = 0.0f;
+                int64_t j = j0;
+                for (; j < hi && spos[j] / chunk == cid; ++j)
+                    part = part + grad_elem(grad[(int64_t)spos[j] * D + d], scale, scale_mode);
+                acc = bf16f(bf16r(acc + bf16f(bf16r(part))));
+                j0 = j;
+            }
+            o = finish(acc, scale, scale_mode);
+        } else if (!empty) {
             float acc = 0.0f;
             for (int64_t j0 = lo; j0 < hi; j0 += kRowsPerPartial) {
                 const int64_t j1 = j0 + kRowsPerPartial < hi ? j0 + kRowsPerPartial : hi;
@@ -440,9 +495,14 @@ int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, i
     size_t lds = 0;
     const int rc = z1detail::occupancy_lds(dev, kEmbWgPerCu, &lds);
     if (rc) return rc;
-    hipLaunchKernelGGL(emb_rows_kernel, dim3((unsigned)V), dim3(kEmbThreads), lds, st, grad, D, w.svals, w.row_lo,
-                       padding_idx, scale, scale_mode, vec, out, w.counts, w.heavy_list, w.heavy_base, w.long_list, w.long_base,
-                       w.run_start);
+    if (R < kSortMinRows)   // aten's kernel for few indices: its order, no heavy passes (nothing is listed for them)
+        hipLaunchKernelGGL(emb_rows_kernel<true>, dim3((unsigned)V), dim3(kEmbThreads), lds, st, grad, D, w.svals,
+                           w.row_lo, padding_idx, scale, scale_mode, vec, out, w.counts, w.heavy_list, w.heavy_base,
+                           w.long_list, w.long_base, w.run_start);
+    else
+        hipLaunchKernelGGL(emb_rows_kernel<false>, dim3((unsigned)V), dim3(kEmbThreads), lds, st, grad, D, w.svals,
+                           w.row_lo, padding_idx, scale, scale_mode, vec, out, w.counts, w.heavy_list, w.heavy_base,
+                           w.long_list, w.long_base, w.run_start);
     e = hipGetLastError();
     if (e != hipSuccess) return (int)e;
     if (vec)

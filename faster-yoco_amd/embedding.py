@@ -4,7 +4,7 @@ The reference forms it on the embedding's owner from every rank's rows with
 ``torch.ops.aten.embedding_dense_backward`` and scales by 1/world: after the call on the all-gathered rows
 (yoco/models/decoder/layer_graphs.py:87-93) or on rows scaled in place first (the copy-engine path,
 yoco/models/decoder/ce_reduce.py:226-231).  ``embedding_dense_backward`` keeps aten's signature and summation order
-(its sort-based GPU path) and fuses the scale; ``owner_embedding_grad`` / ``ce_owner_embedding_grad`` are the two
+(its sort-based path above 3072 indices, its chunked kernel up to 3072) and fuses the scale; ``owner_embedding_grad`` / ``ce_owner_embedding_grad`` are the two
 call sites' forms.
 """
 import torch

@@ -155,8 +155,10 @@ int z1_cast_bf16(const float* p32, uint16_t* p16, int64_t n, void* stream);
 /* The embedding owner's token-embedding gradient: out[V x D] (bf16) = torch.ops.aten.embedding_dense_backward(
  * grad[R x D] (bf16), ids[R] (int64), V, padding_idx, False) with the reference's x 1/world
  * (yoco/models/decoder/layer_graphs.py:87-93: scale after, scale_mode 2; yoco/models/decoder/ce_reduce.py:226-231:
- * rows scaled first, scale_mode 1; 0: no scale).  Same order as aten's sort-based GPU path: each id's occurrences
- * in position order, fp32 partial sums over runs of 10, partials summed in order, one bf16 rounding.  Every row of
+ * rows scaled first, scale_mode 1; 0: no scale).  Same order as aten for the row count.  For R > 3072 its
+ * sort-based path: each id's occurrences in position order, fp32 partial sums over runs of 10, partials summed in
+ * order, one bf16 rounding.  For R <= 3072 its kernel for few indices: chunks of 16 indices, per chunk and id an fp32
+ * sum rounded to bf16 and added to the bf16 row.  Every row of
  * out is written (rows without occurrences, padding_idx and ids outside [0, V) give zeros).  workspace: device
  * memory of z1_embedding_backward_workspace(R, D, V) bytes (with D <= 2^24: about 4/7 of R x D x 4 bytes for
  * the fp32 run partials of frequent ids, and R x 16 + V x 4 bytes plus the radix sort's storage).  */

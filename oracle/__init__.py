@@ -53,6 +53,7 @@ def lib():
         L.oracle_adam_cast.argtypes = [_P, _I, _P, _P, _P, _P, _I64, _F, _I, _F, _F, _F, _F, _F, _F, _F, _I]
         L.oracle_greedy_partition.argtypes = [_P, _I, _I, _P, _P]
         L.oracle_embedding_backward.argtypes = [_P, _P, _I64, _I64, _I64, _I64, _F, _I, _P]
+        L.oracle_embedding_backward_chunked.argtypes = [_P, _P, _I64, _I64, _I64, _I64, _F, _I, _I64, _P]
         _LIB = L
     return _LIB
 
@@ -184,9 +185,22 @@ def adam_cast(g, p, m, v, *, lr, beta1, beta2, eps, weight_decay, step, mode=1, 
     return p, m, v, p16
 
 
+SORT_PATH_MIN_ROWS = 3073         # aten.embedding_dense_backward sorts for more than 3072 indices
+FEW_ROWS_CHUNK = 16               # index chunk of its kernel for fewer (torch's ROCm build, MI355X)
+
+
 def embedding_backward(ids, grad16, num_weights, padding_idx=-1, scale=None, scale_first=False):
-    """aten.embedding_dense_backward's sort-path order (+ the reference's optional 1/world), see z1_oracle.c.
-    ids: int64 [R]; grad16: uint16 bf16 bits [R, D].  Returns uint16 [V, D]."""
+    """aten.embedding_dense_backward (+ the reference's optional 1/world) in aten's order for the row count: the
+    sort-path order for more than 3072 rows, the chunked order for fewer.  ids: int64 [R]; grad16: uint16 bf16 bits
+    [R, D].  Returns uint16 [V, D]."""
+    R = np.asarray(grad16).shape[0]
+    if R >= SORT_PATH_MIN_ROWS:
+        return embedding_backward_sort(ids, grad16, num_weights, padding_idx, scale, scale_first)
+    return embedding_backward_chunked(ids, grad16, num_weights, padding_idx, scale, scale_first)
+
+
+def embedding_backward_sort(ids, grad16, num_weights, padding_idx=-1, scale=None, scale_first=False):
+    """aten's sort-path order at any row count (runs of 10 occurrences), see z1_oracle.c."""
     ids = _c(np.asarray(ids, dtype=np.int64), np.int64)
     g = _c(grad16, np.uint16)
     R, D = g.shape
@@ -194,6 +208,21 @@ def embedding_backward(ids, grad16, num_weights, padding_idx=-1, scale=None, sca
     mode = 0 if scale is None else (1 if scale_first else 2)
     lib().oracle_embedding_backward(_ptr(ids), _ptr(g), R, D, num_weights, padding_idx,
                                     float(np.float32(1.0 if scale is None else scale)), mode, _ptr(out))
+    return out
+
+
+def embedding_backward_chunked(ids, grad16, num_weights, padding_idx=-1, scale=None, scale_first=False,
+                               chunk=FEW_ROWS_CHUNK):
+    """aten's order for few rows at any row count (chunks of `chunk` indices, per-chunk bf16 rounding), see
+    z1_oracle.c."""
+    ids = _c(np.asarray(ids, dtype=np.int64), np.int64)
+    g = _c(grad16, np.uint16)
+    R, D = g.shape
+    out = np.empty((num_weights, D), dtype=np.uint16)
+    mode = 0 if scale is None else (1 if scale_first else 2)
+    lib().oracle_embedding_backward_chunked(_ptr(ids), _ptr(g), R, D, num_weights, padding_idx,
+                                            float(np.float32(1.0 if scale is None else scale)), mode, int(chunk),
+                                            _ptr(out))
     return out
 
 

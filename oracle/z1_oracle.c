@@ -244,6 +244,39 @@ void oracle_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t
     }
 }
 
+/* The same gradient in the order of aten's kernel for few indices (embedding_dense_backward takes it for at most 3072
+ * indices, the sort-based path above otherwise): positions in chunks of `chunk` consecutive indices; per chunk and id
+ * the fp32 sum of that id's rows in position order, rounded to bf16 and added to the bf16 row of grad_weight (an fp32
+ * add rounded to bf16).  chunk = 16 is what torch's ROCm build does on MI355X (checked against it on the GPU). */
+void oracle_embedding_backward_chunked(const int64_t* ids, const uint16_t* grad, int64_t R, int64_t D, int64_t V,
+                                       int64_t padding_idx, float scale, int scale_mode, int64_t chunk,
+                                       uint16_t* out) {
+    for (int64_t t = 0; t < V; ++t) {
+        for (int64_t d = 0; d < D; ++d) {
+            uint16_t acc = 0;
+            int none = 1;
+            for (int64_t c0 = 0; c0 < R; c0 += chunk) {
+                float part = 0.0f;
+                int any = 0;
+                for (int64_t r = c0; r < R && r < c0 + chunk; ++r) {
+                    if (ids[r] != t) continue;
+                    float x = bf16_to_f32(grad[r * D + d]);
+                    if (scale_mode == 1) x = bf16_to_f32(oracle_bf16_rne(x * scale));
+                    part = part + x;
+                    any = 1;
+                }
+                if (any) {
+                    acc = oracle_bf16_rne(bf16_to_f32(acc) + bf16_to_f32(oracle_bf16_rne(part)));
+                    none = 0;
+                }
+            }
+            uint16_t o = acc;
+            if (scale_mode == 2) o = oracle_bf16_rne(bf16_to_f32(o) * scale);
+            out[t * D + d] = (t == padding_idx || none) ? 0 : o;
+        }
+    }
+}
+
 /* zero1_fast.py:61-65: params in order, each to the rank with the smallest running total (first such rank). */
 void oracle_greedy_partition(const int64_t* numel, int nparam, int world, int32_t* owner, int64_t* sizes) {
     for (int r = 0; r < world; ++r) sizes[r] = 0;

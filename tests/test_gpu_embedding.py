@@ -1,6 +1,7 @@
 """The owner's token-embedding gradient on the GPU, against torch's own aten.embedding_dense_backward on the same
 device (the routine the reference calls, yoco/models/decoder/layer_graphs.py:92, ce_reduce.py:230) and against the
-oracle.  aten takes its sort-based path for more than 3072 indices; that is the order restated here (bit-exact)."""
+oracle.  aten takes its sort-based path for more than 3072 indices and another kernel for fewer; this build follows
+the order of each (bit-exact)."""
 import numpy as np
 import pytest
 import torch
@@ -78,6 +79,29 @@ def test_heavy_ids_at_the_run_boundaries(pkg, dev, D):
             got = embedding.embedding_dense_backward(g, ids, V, pad)
             torch.cuda.synchronize()
             assert np.array_equal(bits(got), bits(ref)), (R, pad)
+
+
+@pytest.mark.parametrize('D', [3072, 40, 13])
+def test_matches_aten_at_3072_rows_or_fewer(pkg, dev, D):
+    """At most 3072 rows: aten's kernel for few indices, whose order (chunks of 16 indices, each chunk's sum rounded to
+    bf16 and added to the bf16 row) this build follows there.  Bit-exact against torch's aten for 1 row, for chunk
+    boundaries (15, 16, 17 rows), and up to 3072 rows with heavy repeats, padding and both 1/world placements."""
+    from faster_yoco_amd import embedding
+    rng = np.random.default_rng(100 + D)
+    for R, V in ((1, 5), (15, 3), (16, 3), (17, 3), (1000, 7), (2048, 300), (3072, 40), (3072, 100288)):
+        ids = torch.from_numpy(rng.integers(0, V, R).astype(np.int64)).to(dev)
+        g = (torch.randn(R, D, device=dev) * 1e-2).to(torch.bfloat16)
+        for pad in (-1, 2):
+            ref = torch.ops.aten.embedding_dense_backward(g, ids, V, pad, False)
+            got = embedding.embedding_dense_backward(g, ids, V, pad)
+            torch.cuda.synchronize()
+            assert np.array_equal(bits(got), bits(ref)), (R, V, pad)
+        ref2 = torch.ops.aten.embedding_dense_backward(g, ids, V, -1, False).mul_(1.0 / 8)
+        ref3 = torch.ops.aten.embedding_dense_backward(g.clone().mul_(1.0 / 8), ids, V, -1, False)
+        got2 = embedding.owner_embedding_grad(g, ids, V, -1, 8)
+        got3 = embedding.ce_owner_embedding_grad(g, ids, V, -1, 8)
+        torch.cuda.synchronize()
+        assert np.array_equal(bits(got2), bits(ref2)) and np.array_equal(bits(got3), bits(ref3)), R
 
 
 def test_matches_oracle_and_edge_cases(pkg, dev):

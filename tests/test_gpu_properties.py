@@ -134,7 +134,8 @@ def test_norm_random_tables(pkg, dev, sizes, offs, g_bf16, mag, max_norm, factor
        bad=st.integers(0, 20), seed=st.integers(0, 2 ** 31 - 1))
 def test_embedding_random(pkg, dev, R, D, V, pad, mode, world, bad, seed):
     """Embedding gradient for random ids (repeats, out-of-range ids, padding), widths (incl. D % 8 != 0) and both
-    placements of the 1/world scale: bit-exact against the oracle's restatement of aten's sort-path order."""
+    placements of the 1/world scale: bit-exact against the oracle's restatement of aten's order for the row count
+    (the sort path above 3072 rows, chunks of 16 indices up to it)."""
     from faster_yoco_amd import embedding
     rng = np.random.default_rng(seed)
     pad = pad if pad < V else -1

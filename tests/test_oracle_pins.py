@@ -351,9 +351,30 @@ def test_embedding_backward_sums_in_runs_of_ten():
     10 x 2^-24 and the result rounds up to 1 + 2^-7."""
     vals = [1.0, 2.0 ** -8] + [2.0 ** -24] * 18
     g = oracle.bf16_rne(np.array(vals, np.float32).reshape(-1, 1))
-    out = oracle.embedding_backward(np.zeros(len(vals), np.int64), g, 1)
+    out = oracle.embedding_backward_sort(np.zeros(len(vals), np.int64), g, 1)
     assert out[0, 0] == 0x3F81
     seq = np.float32(0.0)
     for v in vals:
         seq = np.float32(seq + np.float32(v))
     assert torch_bf16_bits(np.array([seq], np.float32))[0] == 0x3F80
+
+
+def test_embedding_backward_chunks_of_sixteen_below_the_sort_threshold():
+    """aten's kernel for at most 3072 indices rounds each chunk's sum to bf16 before adding it to the bf16 row.  On
+    one id, rows 1.0, 2^-9, fourteen zeros, 2^-8: chunks of 16 give bf16(1 + 2^-9) = 1.0 (a quarter ulp), then
+    bf16(1.0 + 2^-8) = 1.0 (a tie, to even): 0x3F80.  One chunk of 32, and the sort path's runs of 10 (1 + 2^-9, then
+    2^-8, summed in fp32), give bf16(1 + 3 * 2^-9) = 1 + 2^-7 (three quarters of an ulp, up): 0x3F81."""
+    vals = [1.0, 2.0 ** -9] + [0.0] * 14 + [2.0 ** -8]
+    g = oracle.bf16_rne(np.array(vals, np.float32).reshape(-1, 1))
+    ids = np.zeros(len(vals), np.int64)
+    assert oracle.embedding_backward_chunked(ids, g, 1)[0, 0] == 0x3F80
+    assert oracle.embedding_backward_chunked(ids, g, 1, chunk=32)[0, 0] == 0x3F81
+    assert oracle.embedding_backward_sort(ids, g, 1)[0, 0] == 0x3F81
+    assert oracle.embedding_backward(ids, g, 1)[0, 0] == 0x3F80          # 17 rows: aten's few-rows kernel
+    # the dispatch follows aten's threshold: more than 3072 rows take the sort path
+    rng = np.random.default_rng(3)
+    for R in (3072, 3073):
+        ids = rng.integers(0, 5, R).astype(np.int64)
+        g = oracle.bf16_rne((rng.standard_normal((R, 3)) * 1e-2).astype(np.float32))
+        want = (oracle.embedding_backward_sort if R > 3072 else oracle.embedding_backward_chunked)(ids, g, 5)
+        assert np.array_equal(oracle.embedding_backward(ids, g, 5), want)
