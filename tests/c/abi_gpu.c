@@ -4,8 +4,11 @@
  *   1. a 4-row table (tails, a row below one chunk, 64-element row alignment): sum of squares -> norm + clip
  *      -> Adam + BF16 copy with the device factor; norm within 1e-6 of the exact one, the clip chain bit-exact
  *      from the GPU's norm, p / m / v / BF16 bit-exact given the GPU's factor;
+ *      A second step runs as two launches over row ranges (z1_adam_cast_rows), again bit-exact;
  *   2. the owner sum of 8 BF16 contributions with the fused norm: average and FP32 sum bit-exact, norm within
- *      1e-6 of the average's exact norm.
+ *      1e-6 of the average's exact norm;
+ *   3. the embedding gradient (workspace query, ids with repeats, out-of-range ids and padding, x 1/8 after) at
+ *      5000 rows (aten's sort-path order) and 1000 rows (its order for few indices): bit-exact.
  * Built by __graft_entry__.build() with gcc, linked against libyoco_z1.so, the oracle and the HIP runtime, twice:
  * as tests/c/libabi_gpu.so, whose abi_gpu_run() tests/test_gpu_c_abi.py calls in-process, and with -DABI_GPU_MAIN
  * as the standalone program tests/c/abi_gpu.  Returns (exits with) 0 and prints "ok" on success. */
@@ -29,6 +32,11 @@ void oracle_bias_corrections(double beta1, double beta2, int64_t step, int bias_
 void oracle_adam_cast(const void* g, int g_bf16, float* p, float* m, float* v, uint16_t* p16, int64_t n,
                       float factor, int apply_factor, float lr, float beta1, float beta2, float eps, float bc1,
                       float bc2, float wd, int mode);
+void oracle_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, int64_t D, int64_t V,
+                               int64_t padding_idx, float scale, int scale_mode, uint16_t* out);
+void oracle_embedding_backward_chunked(const int64_t* ids, const uint16_t* grad, int64_t R, int64_t D, int64_t V,
+                                       int64_t padding_idx, float scale, int scale_mode, int64_t chunk,
+                                       uint16_t* out);
 
 #define HIP_OK(x)                                                                                   \
     do {                                                                                            \
@@ -153,6 +161,24 @@ static int table_update(void) {
         EXPECT(same_f32(op + o, hp + o, n) && same_f32(om + o, hm + o, n) && same_f32(ov + o, hv + o, n));
         EXPECT(memcmp(o16 + o, h16 + o, (size_t)n * 2) == 0);
     }
+    /* step 1001 from that state as two launches over row ranges, the factor 0.75 on the host side */
+    oracle_bias_corrections(0.9, 0.95, step + 1, 1, bc);
+    const float f2 = 0.75f;
+    HIP_OK(hipMemcpy(ds + 2, &f2, 4, hipMemcpyHostToDevice));
+    EXPECT(z1_adam_cast_rows(t, 3, 5, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL) == Z1_E_SIZE);
+    Z1_OK_(z1_adam_cast_rows(t, 0, 1, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL));
+    Z1_OK_(z1_adam_cast_rows(t, 1, R, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL));
+    HIP_OK(hipDeviceSynchronize());
+    HIP_OK(hipMemcpy(op, dp, total * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(om, dm, total * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(ov, dv, total * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(o16, d16, total * 2, hipMemcpyDeviceToHost));
+    for (int i = 0; i < R; ++i) {
+        const int64_t o = off[i], n = sizes[i];
+        oracle_adam_cast(hg + o, 0, hp + o, hm + o, hv + o, h16 + o, n, f2, 1, lr, b1, b2, eps, bc[0], bc[1], wd, 1);
+        EXPECT(same_f32(op + o, hp + o, n) && same_f32(om + o, hm + o, n) && same_f32(ov + o, hv + o, n));
+        EXPECT(memcmp(o16 + o, h16 + o, (size_t)n * 2) == 0);
+    }
     Z1_OK_(z1_table_destroy(t));
     HIP_OK(hipFree(dg));
     HIP_OK(hipFree(dp));
@@ -209,9 +235,49 @@ static int owner_sum(void) {
     return 0;
 }
 
+static int embedding_grad(int64_t R) {
+    const int64_t D = 40, V = 300, pad = 7;
+    int64_t* hid = malloc(R * 8);
+    uint16_t *hgr = malloc(R * D * 2), *hout = malloc(V * D * 2), *want = malloc(V * D * 2);
+    for (int64_t i = 0; i < R; ++i) {
+        const double u = unif();
+        hid[i] = (int64_t)(u * u * V);           /* skewed: low ids repeat often, id 0 more than 20 times */
+        if (i % 97 == 5) hid[i] = (i % 2) ? -3 : V + 11;      /* outside [0, V): ignored */
+    }
+    for (int64_t i = 0; i < R * D; ++i) hgr[i] = oracle_bf16_rne(normal(1e-2));
+    const int64_t ws = z1_embedding_backward_workspace(R, D, V);
+    EXPECT(ws > 0);
+    int64_t* did;
+    uint16_t *dgr, *dout;
+    void* dws;
+    HIP_OK(hipMalloc((void**)&did, R * 8));
+    HIP_OK(hipMalloc((void**)&dgr, R * D * 2));
+    HIP_OK(hipMalloc((void**)&dout, V * D * 2));
+    HIP_OK(hipMalloc(&dws, (size_t)ws));
+    HIP_OK(hipMemcpy(did, hid, R * 8, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dgr, hgr, R * D * 2, hipMemcpyHostToDevice));
+    EXPECT(z1_embedding_backward(did, dgr, R, D, V, pad, 0.125f, 2, dout, dws, ws - 1, NULL) == Z1_E_WORKSPACE);
+    Z1_OK_(z1_embedding_backward(did, dgr, R, D, V, pad, 0.125f, 2, dout, dws, ws, NULL));
+    HIP_OK(hipDeviceSynchronize());
+    HIP_OK(hipMemcpy(hout, dout, V * D * 2, hipMemcpyDeviceToHost));
+    if (R > 3072)
+        oracle_embedding_backward(hid, hgr, R, D, V, pad, 0.125f, 2, want);
+    else
+        oracle_embedding_backward_chunked(hid, hgr, R, D, V, pad, 0.125f, 2, 16, want);
+    EXPECT(memcmp(hout, want, (size_t)(V * D * 2)) == 0);
+    HIP_OK(hipFree(did));
+    HIP_OK(hipFree(dgr));
+    HIP_OK(hipFree(dout));
+    HIP_OK(hipFree(dws));
+    free(hid); free(hgr); free(hout); free(want);
+    return 0;
+}
+
 int abi_gpu_run(void) {
     int rc = table_update();
     if (rc == 0) rc = owner_sum();
+    if (rc == 0) rc = embedding_grad(5000);
+    if (rc == 0) rc = embedding_grad(1000);
     printf("%s\n", rc ? "FAIL" : "ok");
     fflush(stdout);
     return rc;
