@@ -357,6 +357,7 @@ def main():
     ends = [e[0] for e in events[1:]] + [last]
     adam_ms = [e[1].elapsed_time(end) for e, end in zip(events, ends)]
     pre_ms = [e[0].elapsed_time(e[1]) for e in events]
+    step_ms = sorted(e[0].elapsed_time(end) for e, end in zip(events, ends))      # GPU time of each step
     adam_avg = sum(adam_ms) / len(adam_ms)
     n = shard.numel
     step_bytes, adam_bytes, adam_bpp = algorithmic_bytes(cfg, n)
@@ -378,6 +379,7 @@ def main():
                    'grad_dtype': str(gdt).replace('torch.', ''), 'lr': hp['lr'], 'betas': list(hp['betas']),
                    'eps': hp['eps'], 'weight_decay': hp['weight_decay'], 'max_norm': hp['max_norm'],
                    'algorithmic_bytes_per_step': step_bytes},
+        'median_step_ms_events': round(step_ms[len(step_ms) // 2], 4),
         'achieved_GBps': round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
         'frac_of_peak': round(step_bytes / (ms_step * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
         'kernel_ms': {'adam_cast': round(adam_avg, 4),
