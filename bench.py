@@ -1,8 +1,8 @@
 """Benchmark of the ZeRO-1 shard optimizer update on one MI355X.
 
-A step is one optimizer update of one GPU's shard with its inputs resident in HBM: sum of squares -> norm + clip
-factor -> Adam + BF16 copy (config c3 adds the fused owner sum of 8 BF16 contributions in front, replacing the
-sum of squares).  Default workload: c2, the 430,662,912-parameter YOCO-3B shard (the configuration the metric is
+A step is one optimizer update of one GPU's shard with its inputs resident in HBM: the norm -> its final reduction
++ the clip factor -> Adam + BF16 copy (config c3: the owner sum of 8 BF16 contributions with the norm fused in, then
+the final reduction + clip factor, then Adam).  Default workload: c2, the 430,662,912-parameter YOCO-3B shard (the configuration the metric is
 quoted on).
 
 Prints ONE JSON line: ms per step (the metric), the Adam kernel's roofline from HIP events recorded on the
@@ -329,35 +329,36 @@ def main():
         print(f'# cpu baseline done: {cpu["sample"]}', file=sys.stderr, flush=True)
 
     def one_step(ev=None):
-        # two events per step: ev[0] before the norm pass, ev[1] before Adam; the next step's ev[0] (or the final
-        # event) closes Adam.  Each record costs about 2.5 us of step time, so no third one.
+        # a sampled step records three events: before the norm pass, before Adam, after Adam (each record costs
+        # about 2.5 us of GPU time, so only every `every`-th step of the timed region carries them)
         if ev is not None:
             ev[0].record()
         if contribs is not None:
-            opt.reduce_grads(contribs)
-        opt.clip_grad_norm(hp['max_norm'])
+            opt.reduce_clip(contribs, hp['max_norm'])      # owner sum + fused norm, then the clip chain
+        else:
+            opt.clip_grad_norm(hp['max_norm'])              # norm, then its final reduction + clip chain
         if ev is not None:
             ev[1].record()
         opt.step()
+        if ev is not None:
+            ev[2].record()
 
     for _ in range(args.warmup):
         one_step()
     torch.cuda.synchronize()
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
-    last = torch.cuda.Event(enable_timing=True)
+    every = max(1, args.steps // 10)
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(0, args.steps, every)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        one_step(events[i])
-    last.record()
+        one_step(events[i // every] if i % every == 0 else None)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
     ms_step = wall * 1e3 / args.steps
-    ends = [e[0] for e in events[1:]] + [last]
-    adam_ms = [e[1].elapsed_time(end) for e, end in zip(events, ends)]
+    adam_ms = [e[1].elapsed_time(e[2]) for e in events]
     pre_ms = [e[0].elapsed_time(e[1]) for e in events]
-    step_ms = sorted(e[0].elapsed_time(end) for e, end in zip(events, ends))      # GPU time of each step
+    step_ms = sorted(e[0].elapsed_time(e[2]) for e in events)      # GPU time of each sampled step
     adam_avg = sum(adam_ms) / len(adam_ms)
     n = shard.numel
     step_bytes, adam_bytes, adam_bpp = algorithmic_bytes(cfg, n)
@@ -380,10 +381,11 @@ def main():
                    'eps': hp['eps'], 'weight_decay': hp['weight_decay'], 'max_norm': hp['max_norm'],
                    'algorithmic_bytes_per_step': step_bytes},
         'median_step_ms_events': round(step_ms[len(step_ms) // 2], 4),
+        'event_sampled_steps': len(events),
         'achieved_GBps': round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
         'frac_of_peak': round(step_bytes / (ms_step * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
         'kernel_ms': {'adam_cast': round(adam_avg, 4),
-                      ('owner_sum+norm_clip' if cfg == 'c3' else 'sumsq+norm_clip'):
+                      ('owner_sum+norm_clip' if cfg == 'c3' else 'norm_clip'):
                           round(sum(pre_ms) / len(pre_ms), 4)},
         'roofline': {'bound': 'hbm', 'kernel': 'adam_cast_kernel', 'achieved': round(achieved, 1),
                      'peak': PEAK_HBM_GBPS, 'unit': 'GB/s', 'frac': round(achieved / PEAK_HBM_GBPS, 4),

@@ -44,7 +44,11 @@ SIGNATURES = {
     'z1_table_info': ([_P, ctypes.POINTER(_I64), ctypes.POINTER(_I64), ctypes.POINTER(_I)], _I),
     'z1_owner_sum_bf16': ([_P, _I, _I64, _F, _P, _P, _P, _P], _I),
     'z1_owner_sum_workspace': ([_I64], _I64),
+    'z1_owner_sum_update': ([_P, _I, _I64, _F, _P, _P, _P, ctypes.POINTER(Z1UpdateScalars), _P], _I),
+    'z1_table_set_grads': ([_P, _P, _I, _P], _I),
     'z1_grad_sumsq': ([_P, _P, _P], _I),
+    'z1_grad_norm_clip': ([_P, _P, _P, _F, _P, _P, _P, _F, _P], _I),
+    'z1_grad_update_scalars': ([_P, _P, ctypes.POINTER(Z1UpdateScalars), _P], _I),
     'z1_norm_clip': ([_P, _P, _F, _P, _P, _P, _F, _P], _I),
     'z1_clip_factor': ([_P, _P, _F, _P, _P, _F, _P], _I),
     'z1_update_scalars_run': ([_P, ctypes.POINTER(Z1UpdateScalars), _P], _I),

@@ -27,10 +27,13 @@
 //     wave per chunk with hardware dispatch (0.40 ms), 4-chunk workgroups with hardware dispatch (0.34 ms),
 //     2-8 loads in flight per wave (0.28-0.31 ms) and fewer waves (0.35-0.59 ms) were all slower.
 //   * MALL reuse between passes: the pass before Adam (the norm, or the owner sum that writes the BF16 average)
-//     touches the last 256 (224) MB of the gradient with ordinary, allocating accesses, and Adam walks the
-//     chunks from the last one, so its first gradient reads hit the 256 MB MALL (measured 2.05 vs 2.10 ms for
-//     Adam on the C2 shard; 128-512 MB kept, or everything, measured the same or slower).
-//   * No atomics anywhere; nothing but vector memory instructions write memory.
+//     touches 256 (224) MB of the gradient with ordinary, allocating accesses where Adam starts, and Adam walks
+//     the chunks from the last one, so its first gradient reads hit the 256 MB MALL (measured 2.05 vs 2.10 ms for
+//     Adam on the C2 shard; 128-512 MB kept, or everything, measured the same or slower).  The norm keeps the top
+//     of each XCD's eighth, where that XCD's Adam workgroups start.
+//   * No atomics anywhere; nothing but vector memory instructions write memory.  (The norm's final reduction is a
+//     second, one-workgroup launch: folding it into the last workgroup of the norm grid to finish, with an arrival
+//     counter, measured 75 us slower per step, because the grid's 2048 workgroups finish together.)
 //
 // Numerics follow the header: one rounding per fp32 operation, explicit FMAs where the reference has them,
 // correctly rounded division and square root (built with -fhip-fp32-correctly-rounded-divide-sqrt, no fast math,
@@ -84,7 +87,7 @@ struct Row {
     int64_t n;
     int64_t chunk0;
     int32_t vec;        // bit 0: g aligned for the vector path; bit 1: p, m, v, p16 aligned as well
-    int32_t pad;
+    int32_t pmv_aligned;    // p, m, v, p16 aligned for the vector path (vec's bit 1 needs g aligned too)
 };
 static_assert(sizeof(Row) == 64, "row layout");
 
@@ -268,6 +271,64 @@ __device__ __forceinline__ double sq64(float x) {
     return d * d;                      // exact: 24-bit significand squared
 }
 
+// zero1_fast.py:150-160 scalar chain, one owner.
+__device__ __forceinline__ void clip_chain(float norm, float fac, float* grad_norm_out, float* factor_out,
+                                           float max_norm) {
+    const float gn = fac * norm;
+    if (grad_norm_out) *grad_norm_out = gn;
+    float f = fac;
+    if (max_norm > 0.0f) {
+        const float t = gn + 1e-6f;
+        float coef = (1.0f / t) * max_norm;
+        coef = (coef > 1.0f) ? 1.0f : coef;           // clamp(max=1), NaN stays NaN
+        f = fac * coef;
+    }
+    if (factor_out) *factor_out = f;
+}
+
+// The Z1_NORM_PARTIALS partials summed in one fixed order (strided per thread, then the workgroup tree); the total
+// is valid in thread 0.  Every final reduction of the norm goes through here, so its bits do not depend on which
+// kernel runs it.
+__device__ __forceinline__ double final_sum(const double* partials, double* lds) {
+    double s = 0.0;
+    for (int i = threadIdx.x; i < Z1_NORM_PARTIALS; i += kThreads) s += partials[i];
+    return block_sum(s, lds);
+}
+
+// Thread 0, given the exact sum of squares: the norm / clip chain of zero1_fast.py:150-160, preceded, for the
+// trainer's form, by the sample-size factor of trainer_nosync.py:273-279 and followed by the deferred-check flags
+// and the "clip" metric (:284-286, :194-197).  With u.sample_size, u.flags_out and u.clip_log_out all NULL this is
+// exactly the z1_norm_clip chain.
+__device__ __forceinline__ void scalar_tail(double tot, const z1_update_scalars& u) {
+    float fac = u.factor_in ? *u.factor_in : u.factor_value;
+    if (u.sample_size) {
+        // multiply_grads(numer / where(ss > 0, ss, 1)): `int / tensor` is reciprocal(tensor) * int in torch
+        const float ss = *u.sample_size;
+        const float denom = (ss > 0.0f) ? ss : 1.0f;
+        const float c = (1.0f / denom) * u.numer;
+        fac = c * fac;
+    }
+    const float nr = (float)__builtin_sqrt(tot);      // the fp32 norm clip_grad_norm_ returns
+    const float sq = nr * nr;                          // .float() ** 2 (all_reduce over one owner: identity)
+    const float norm = __builtin_sqrtf(sq);
+    if (u.norm_out) *u.norm_out = nr;
+    const float gn = fac * norm;
+    clip_chain(norm, fac, u.grad_norm_out, u.factor_out, u.max_norm);
+    if (u.flags_out) {
+        const uint32_t b = __float_as_uint(gn) & 0x7fffffffu;
+        u.flags_out[0] = b < 0x7f800000u ? 1 : 0;       // isfinite(grad_norm)
+        u.flags_out[1] = 1;                               // one owner: consistent with itself
+    }
+    if (u.clip_log_out && u.max_norm > 0.0f) *u.clip_log_out = gn > u.max_norm ? 100.0f : 0.0f;
+}
+
+// One workgroup: the final reduction and the scalar tail (z1_norm_clip, z1_update_scalars_run).
+__global__ __launch_bounds__(kThreads) void scalars_kernel(const double* __restrict__ partials, z1_update_scalars u) {
+    __shared__ double lds[kThreads / kWave];
+    const double tot = final_sum(partials, lds);
+    if (threadIdx.x == 0) scalar_tail(tot, u);
+}
+
 // Last row whose first chunk is <= c, searching forward from row t (c only grows within a wave).  The rows table
 // is a few KiB and stays in the scalar cache; the chunk -> row map is not read here (it would add ~3% traffic).
 __device__ __forceinline__ int advance_row(const Row* __restrict__ rows, int nrows, int t, int64_t c) {
@@ -302,10 +363,12 @@ __device__ __forceinline__ void sumsq_chunk(const Row& r, int64_t c, int lane, d
 // Fixed grid of Z1_NORM_PARTIALS workgroups (a multiple of 8): the 256 workgroups b with b & 7 == x cover eighth x
 // of the chunks, wave w of them taking chunks lo_x + w, lo_x + w + 1024, ... (a workgroup covers 4 consecutive
 // chunks = 1024 contiguous elements per step); each lane adds its exact squares in that fixed order.
-// Chunks from keep_from on are read with ordinary loads (two loops, so that the two kinds of load stay apart).
+// The last keep_per_eighth chunks of each eighth are read with ordinary loads (two loops, so that the two kinds of
+// load stay apart): they are where the Adam pass of each XCD starts (adam_cast_kernel walks every eighth from its
+// top), so every XCD's first gradient reads hit the MALL.
 template <int GDT>
 __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__ rows, int nrows, int64_t nchunks,
-                                                         int64_t keep_from, double* __restrict__ partials) {
+                                                         int64_t keep_per_eighth, double* __restrict__ partials) {
     __shared__ double lds[kThreads / kWave];
     const int lane = threadIdx.x & (kWave - 1);
     // workgroup b strides through eighth (b & 7) of the chunks only: the eighth the XCD it is dispatched to
@@ -316,7 +379,7 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__
     const int64_t lo = x * Q + (x < R ? x : R), hi = lo + Q + (x < R ? 1 : 0);
     const int64_t nw = (int64_t)(gridDim.x >> 3) * (kThreads / kWave);
     const int64_t w0 = lo + j * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int64_t split = keep_from < hi ? keep_from : hi;
+    const int64_t split = hi - keep_per_eighth > lo ? hi - keep_per_eighth : lo;
     double acc = 0.0;
     int t = 0;
     int64_t c = w0;
@@ -330,71 +393,6 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__
     }
     const double s = block_sum(acc, lds);
     if (threadIdx.x == 0) partials[blockIdx.x] = s;
-}
-
-// zero1_fast.py:150-160 scalar chain, one owner.
-__device__ __forceinline__ void clip_chain(float norm, float fac, float* grad_norm_out, float* factor_out,
-                                           float max_norm) {
-    const float gn = fac * norm;
-    if (grad_norm_out) *grad_norm_out = gn;
-    float f = fac;
-    if (max_norm > 0.0f) {
-        const float t = gn + 1e-6f;
-        float coef = (1.0f / t) * max_norm;
-        coef = (coef > 1.0f) ? 1.0f : coef;           // clamp(max=1), NaN stays NaN
-        f = fac * coef;
-    }
-    if (factor_out) *factor_out = f;
-}
-
-__global__ __launch_bounds__(kThreads) void norm_clip_kernel(const double* __restrict__ partials,
-                                                             const float* factor_in, float factor_value,
-                                                             float* norm_out, float* grad_norm_out, float* factor_out,
-                                                             float max_norm) {
-    __shared__ double lds[kThreads / 64];
-    double s = 0.0;
-    for (int i = threadIdx.x; i < Z1_NORM_PARTIALS; i += kThreads) s += partials[i];
-    const double tot = block_sum(s, lds);
-    if (threadIdx.x == 0) {
-        const float nr = (float)__builtin_sqrt(tot);  // the fp32 norm clip_grad_norm_ returns
-        const float sq = nr * nr;                      // .float() ** 2 (all_reduce over one owner: identity)
-        const float norm = __builtin_sqrtf(sq);
-        if (norm_out) *norm_out = nr;
-        clip_chain(norm, factor_in ? *factor_in : factor_value, grad_norm_out, factor_out, max_norm);
-    }
-}
-
-// The trainer's per-update scalars in one kernel (yoco/tasks/trainer_nosync.py:273-286, zero1_fast.py:150-160,
-// and the "clip" metric of trainer_nosync.py:194-197): the sample-size factor, the norm / clip chain, the deferred
-// check flags and the logging constant.
-__global__ __launch_bounds__(kThreads) void update_scalars_kernel(const double* __restrict__ partials,
-                                                                  z1_update_scalars u) {
-    __shared__ double lds[kThreads / kWave];
-    double s = 0.0;
-    for (int i = threadIdx.x; i < Z1_NORM_PARTIALS; i += kThreads) s += partials[i];
-    const double tot = block_sum(s, lds);
-    if (threadIdx.x == 0) {
-        float fac = u.factor_in ? *u.factor_in : u.factor_value;
-        if (u.sample_size) {
-            // multiply_grads(numer / where(ss > 0, ss, 1)): `int / tensor` is reciprocal(tensor) * int in torch
-            const float ss = *u.sample_size;
-            const float denom = (ss > 0.0f) ? ss : 1.0f;
-            const float c = (1.0f / denom) * u.numer;
-            fac = c * fac;
-        }
-        const float nr = (float)__builtin_sqrt(tot);
-        const float sq = nr * nr;
-        const float norm = __builtin_sqrtf(sq);
-        if (u.norm_out) *u.norm_out = nr;
-        const float gn = fac * norm;
-        clip_chain(norm, fac, u.grad_norm_out, u.factor_out, u.max_norm);
-        if (u.flags_out) {
-            const uint32_t b = __float_as_uint(gn) & 0x7fffffffu;
-            u.flags_out[0] = b < 0x7f800000u ? 1 : 0;       // isfinite(grad_norm)
-            u.flags_out[1] = 1;                               // one owner: consistent with itself
-        }
-        if (u.clip_log_out && u.max_norm > 0.0f) *u.clip_log_out = gn > u.max_norm ? 100.0f : 0.0f;
-    }
 }
 
 // The step counter and bias corrections on the device (z1_bias_corrections_step): ++*step; bc = fp32(1 - beta^step)
@@ -521,6 +519,26 @@ void launch_owner_sum(int world, int64_t nchunks, int64_t keep_from, size_t lds,
     }
 }
 
+// ------------------------------------------------------------------------------------------ gradient rebinding
+// New gradient addresses for up to kBindPerLaunch rows of a table (z1_table_set_grads), passed by value in the
+// kernel arguments, so rebinding is stream-ordered and needs neither an allocation nor a host synchronisation.
+constexpr int kBindPerLaunch = 128;
+struct GradBind {
+    const void* g[kBindPerLaunch];
+    int32_t row[kBindPerLaunch];
+    int32_t count;
+    int32_t g_align;
+};
+
+__global__ __launch_bounds__(kBindPerLaunch) void set_grads_kernel(Row* rows, GradBind b) {
+    const int i = threadIdx.x;
+    if (i >= b.count) return;
+    Row* r = rows + b.row[i];
+    const bool ga = (reinterpret_cast<uintptr_t>(b.g[i]) & (uintptr_t)(b.g_align - 1)) == 0;
+    r->g = b.g[i];
+    r->vec = ga ? (kVecG | (r->pmv_aligned ? kVecAll : 0)) : 0;
+}
+
 // ------------------------------------------------------------------------------------- scale / cast passes
 __global__ __launch_bounds__(kThreads) void scale_up_kernel(const uint16_t* __restrict__ g16, float* __restrict__ g32,
                                                             const float* __restrict__ factor, int64_t n, int vec) {
@@ -628,10 +646,12 @@ inline int launch_status() {
 }  // namespace
 
 struct z1_table {
-    Row* rows;            // device: nrows rows, then nchunks int32 chunk -> row entries (one allocation)
+    Row* rows;            // device, one allocation: the non-empty rows, then nchunks int32 chunk -> row entries
     int32_t* chunk_row;
     std::vector<int64_t> first_chunk;   // host: first chunk of each row given to z1_table_create, + the total
-    int nrows;
+    std::vector<int32_t> dev_row;       // host: device row of each row given to z1_table_create (-1: empty)
+    int nrows;            // rows given to z1_table_create, empty ones included
+    int nrows_dev;        // non-empty rows (the device table)
     int g_dtype;
     int device;
     int has_pmv;          // every row has p, m and v
@@ -665,6 +685,7 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     std::vector<Row> h;
     h.reserve(nrows);
     std::vector<int64_t> first((size_t)nrows + 1);
+    std::vector<int32_t> dev_row((size_t)nrows, -1);
     int64_t chunks = 0, numel = 0;
     int has_pmv = 1;
     for (int i = 0; i < nrows; ++i) {
@@ -681,17 +702,13 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
         r.p16 = t.p16;
         r.n = t.n;
         r.chunk0 = chunks;
-        r.vec = 0;
-        r.pad = 0;
-        if (aligned(t.g, galign)) {
-            r.vec |= kVecG;
-            if (aligned(t.p, 16) && aligned(t.m, 16) && aligned(t.v, 16) && (!t.p16 || aligned(t.p16, 8)))
-                r.vec |= kVecAll;
-        }
+        r.pmv_aligned = aligned(t.p, 16) && aligned(t.m, 16) && aligned(t.v, 16) && (!t.p16 || aligned(t.p16, 8));
+        r.vec = aligned(t.g, galign) ? (kVecG | (r.pmv_aligned ? kVecAll : 0)) : 0;
         if (!t.p || !t.m || !t.v) has_pmv = 0;
         chunks += (t.n + kChunk - 1) / kChunk;
         numel += t.n;
         if (chunks > INT32_MAX) return Z1_E_SIZE;
+        dev_row[i] = (int32_t)h.size();
         h.push_back(r);
     }
     if (chunks > INT32_MAX) return Z1_E_SIZE;          // one workgroup per chunk: grid.x limit
@@ -701,7 +718,7 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     if (rc) return rc;
     // host image of [rows][chunk -> row], copied in one transfer
     const size_t rows_bytes = sizeof(Row) * h.size();
-    std::vector<unsigned char> img(rows_bytes + sizeof(int32_t) * (size_t)chunks);
+    std::vector<unsigned char> img(rows_bytes + sizeof(int32_t) * (size_t)chunks + 64, 0);
     if (rows_bytes) memcpy(img.data(), h.data(), rows_bytes);
     int32_t* map = reinterpret_cast<int32_t*>(img.data() + rows_bytes);
     for (size_t i = 0; i < h.size(); ++i) {
@@ -710,30 +727,36 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     }
     z1_table* tb = new (std::nothrow) z1_table();
     if (!tb) return (int)hipErrorOutOfMemory;
-    tb->nrows = (int)h.size();
+    tb->nrows = nrows;
+    tb->nrows_dev = (int)h.size();
     tb->g_dtype = g_dtype;
     tb->device = dev;
     tb->has_pmv = has_pmv;
     tb->numel = numel;
     tb->nchunks = chunks;
     tb->first_chunk.swap(first);
+    tb->dev_row.swap(dev_row);
     tb->rows = nullptr;
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(&tb->rows), img.empty() ? 64 : img.size());
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&tb->rows), img.size());
     if (e != hipSuccess) {
         delete tb;
         return (int)e;
     }
     tb->chunk_row = reinterpret_cast<int32_t*>(reinterpret_cast<unsigned char*>(tb->rows) + rows_bytes);
-    if (!img.empty()) {
-        e = hipMemcpy(tb->rows, img.data(), img.size(), hipMemcpyHostToDevice);
-        if (e != hipSuccess) {
-            (void)hipFree(tb->rows);
-            delete tb;
-            return (int)e;
-        }
+    e = hipMemcpy(tb->rows, img.data(), img.size(), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)hipFree(tb->rows);
+        delete tb;
+        return (int)e;
     }
     *out = tb;
     return Z1_OK;
+}
+
+static int check_table_device(const z1_table* table, int* dev) {
+    int rc = current_device(dev);
+    if (rc) return rc;
+    return *dev == table->device ? Z1_OK : Z1_E_DEVICE;
 }
 
 int z1_table_destroy(z1_table* table) {
@@ -751,46 +774,113 @@ int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* 
     if (!table) return Z1_E_NULL;
     if (numel) *numel = table->numel;
     if (nchunks) *nchunks = table->nchunks;
-    if (nrows) *nrows = table->nrows;
+    if (nrows) *nrows = table->nrows;             // the rows given to z1_table_create, empty ones included
     return Z1_OK;
 }
 
-static int check_table_device(const z1_table* table, int* dev) {
-    int rc = current_device(dev);
+int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* stream) {
+    if (!table || (nrows > 0 && !g)) return Z1_E_NULL;
+    if (nrows != table->nrows) return Z1_E_SIZE;
+    int dev = 0;
+    int rc = check_table_device(table, &dev);
     if (rc) return rc;
-    return *dev == table->device ? Z1_OK : Z1_E_DEVICE;
+    GradBind b;
+    b.count = 0;
+    b.g_align = table->g_dtype == Z1_F32 ? 16 : 8;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < nrows; ++i) {
+        if (table->dev_row[i] < 0) continue;
+        if (!g[i]) return Z1_E_NULL;
+    }
+    for (int i = 0; i < nrows; ++i) {
+        if (table->dev_row[i] < 0) continue;
+        b.g[b.count] = g[i];
+        b.row[b.count] = table->dev_row[i];
+        if (++b.count == kBindPerLaunch) {
+            hipLaunchKernelGGL(set_grads_kernel, dim3(1), dim3(kBindPerLaunch), 0, s, table->rows, b);
+            rc = launch_status();
+            if (rc) return rc;
+            b.count = 0;
+        }
+    }
+    if (b.count) {
+        hipLaunchKernelGGL(set_grads_kernel, dim3(1), dim3(kBindPerLaunch), 0, s, table->rows, b);
+        return launch_status();
+    }
+    return Z1_OK;
 }
 
-int z1_grad_sumsq(const z1_table* table, double* partials, void* stream) {
-    if (!table || !partials) return Z1_E_NULL;
+// Chunks of each eighth of a table that the norm reads with allocating loads (kMallKeepBytes of gradient over the 8
+// eighths, see sumsq_kernel).
+static int64_t keep_per_eighth(const z1_table* table) {
+    const int64_t chunk_bytes = kChunk * (table->g_dtype == Z1_F32 ? 4 : 2);
+    return kMallKeepBytes / chunk_bytes / 8;
+}
+
+// The norm kernel over the table, then, with a tail, the one-workgroup final reduction + scalar chain.  (A single
+// launch whose last workgroup to finish runs the tail was measured slower: the 2048 workgroups end together, and
+// their device-scope release fences and same-address counter atomics cost 15-35 us at the end of the grid, against
+// about 4 us for the second launch.)
+static int launch_sumsq(const z1_table* table, double* partials, const z1_update_scalars* tail, void* stream) {
     int dev = 0;
     int rc = check_table_device(table, &dev);
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int64_t chunk_bytes = kChunk * (table->g_dtype == Z1_F32 ? 4 : 2);
-    const int64_t keep = kMallKeepBytes / chunk_bytes;
-    const int64_t keep_from = table->nchunks > keep ? table->nchunks - keep : 0;
+    const int64_t kpe = keep_per_eighth(table);
     if (table->g_dtype == Z1_F32)
         hipLaunchKernelGGL(sumsq_kernel<Z1_F32>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows, table->nchunks, keep_from, partials);
+                           table->nrows_dev, table->nchunks, kpe, partials);
     else
         hipLaunchKernelGGL(sumsq_kernel<Z1_BF16>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows, table->nchunks, keep_from, partials);
+                           table->nrows_dev, table->nchunks, kpe, partials);
+    rc = launch_status();
+    if (rc || !tail) return rc;
+    hipLaunchKernelGGL(scalars_kernel, dim3(1), dim3(kThreads), 0, s, partials, *tail);
     return launch_status();
+}
+
+static z1_update_scalars clip_args(const float* factor_in, float factor_value, float* norm_out, float* grad_norm_out,
+                                   float* factor_out, float max_norm) {
+    z1_update_scalars u;
+    memset(&u, 0, sizeof(u));
+    u.numer = 1.0f;
+    u.factor_in = factor_in;
+    u.factor_value = factor_value;
+    u.max_norm = max_norm;
+    u.norm_out = norm_out;
+    u.grad_norm_out = grad_norm_out;
+    u.factor_out = factor_out;
+    return u;
+}
+
+int z1_grad_sumsq(const z1_table* table, double* partials, void* stream) {
+    if (!table || !partials) return Z1_E_NULL;
+    return launch_sumsq(table, partials, nullptr, stream);
+}
+
+int z1_grad_norm_clip(const z1_table* table, double* partials, const float* factor_in, float factor_value,
+                      float* norm_out, float* grad_norm_out, float* factor_out, float max_norm, void* stream) {
+    if (!table || !partials) return Z1_E_NULL;
+    const z1_update_scalars u = clip_args(factor_in, factor_value, norm_out, grad_norm_out, factor_out, max_norm);
+    return launch_sumsq(table, partials, &u, stream);
+}
+
+int z1_grad_update_scalars(const z1_table* table, double* partials, const z1_update_scalars* u, void* stream) {
+    if (!table || !partials || !u) return Z1_E_NULL;
+    return launch_sumsq(table, partials, u, stream);
 }
 
 int z1_norm_clip(const double* partials, const float* factor_in, float factor_value, float* norm_out,
                  float* grad_norm_out, float* factor_out, float max_norm, void* stream) {
     if (!partials) return Z1_E_NULL;
-    hipLaunchKernelGGL(norm_clip_kernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), partials,
-                       factor_in, factor_value, norm_out, grad_norm_out, factor_out, max_norm);
+    hipLaunchKernelGGL(scalars_kernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), partials,
+                       clip_args(factor_in, factor_value, norm_out, grad_norm_out, factor_out, max_norm));
     return launch_status();
 }
 
 int z1_update_scalars_run(const double* partials, const z1_update_scalars* u, void* stream) {
     if (!partials || !u) return Z1_E_NULL;
-    hipLaunchKernelGGL(update_scalars_kernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), partials,
-                       *u);
+    hipLaunchKernelGGL(scalars_kernel, dim3(1), dim3(kThreads), 0, static_cast<hipStream_t>(stream), partials, *u);
     return launch_status();
 }
 
@@ -874,11 +964,14 @@ int z1_bias_corrections_step(int64_t* step, double beta1, double beta2, int bias
 
 int64_t z1_owner_sum_workspace(int64_t n) {
     if (n < 0) return Z1_E_SIZE;
-    return Z1_NORM_PARTIALS + n / kSumChunk + (n % kSumChunk != 0);
+    return Z1_NORM_PARTIALS + n / kSumChunk + (n % kSumChunk != 0);   // the partials, then one per chunk
 }
 
-int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
-                      float* out_sum, double* sumsq_partials, void* stream) {
+// The owner sum with the fused norm when a workspace is given: the per-wave partials' fixed-order reduction leaves
+// the Z1_NORM_PARTIALS partials in the workspace (z1_owner_sum_bf16), and with a tail the one-workgroup final
+// reduction + scalar chain follows (z1_owner_sum_update).
+static int owner_sum(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                     float* out_sum, double* workspace, const z1_update_scalars* tail, void* stream) {
     if (!contrib) return Z1_E_NULL;
     if (world < 1 || world > Z1_MAX_WORLD) return Z1_E_WORLD;
     if (n < 0) return Z1_E_SIZE;
@@ -894,7 +987,7 @@ int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, floa
     const int64_t nchunks = n / kSumChunk + (n % kSumChunk != 0);
     if (nchunks > INT32_MAX) return Z1_E_SIZE;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    double* wave_partials = sumsq_partials ? sumsq_partials + Z1_NORM_PARTIALS : nullptr;
+    double* wave_partials = workspace ? workspace + Z1_NORM_PARTIALS : nullptr;
     if (nchunks > 0) {
         const int64_t keep = kOwnerSumKeepBytes / (kSumChunk * (int64_t)sizeof(uint16_t));
         const int64_t keep_from = nchunks > keep ? nchunks - keep : 0;
@@ -908,12 +1001,24 @@ int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, floa
         rc = launch_status();
         if (rc) return rc;
     }
-    if (sumsq_partials) {
-        hipLaunchKernelGGL(reduce_partials_kernel, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, st, wave_partials,
-                           nchunks, sumsq_partials);
-        return launch_status();
-    }
-    return Z1_OK;
+    if (!workspace) return Z1_OK;
+    hipLaunchKernelGGL(reduce_partials_kernel, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, st, wave_partials, nchunks,
+                       workspace);
+    int rc = launch_status();
+    if (rc || !tail) return rc;
+    hipLaunchKernelGGL(scalars_kernel, dim3(1), dim3(kThreads), 0, st, workspace, *tail);
+    return launch_status();
+}
+
+int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                      float* out_sum, double* sumsq_partials, void* stream) {
+    return owner_sum(contrib, world, n, scale, out_avg, out_sum, sumsq_partials, nullptr, stream);
+}
+
+int z1_owner_sum_update(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                        float* out_sum, double* workspace, const z1_update_scalars* u, void* stream) {
+    if (!workspace || !u) return Z1_E_NULL;
+    return owner_sum(contrib, world, n, scale, out_avg, out_sum, workspace, u, stream);
 }
 
 int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n, void* stream) {

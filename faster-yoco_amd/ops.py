@@ -44,6 +44,8 @@ class Table:
                               p16.data_ptr() if p16 is not None else None, int(n))
         self.g_dtype = Z1_F32 if gd is None else gd
         self.nrows = len(rows)
+        self.sizes = tuple(int(r[5]) for r in rows)
+        self.grad_ptrs = tuple(r[0].data_ptr() for r in rows)      # the gradients the device rows point at now
         h = ctypes.c_void_p()
         with torch.cuda.device(self.device):
             check(lib().z1_table_create(arr, len(rows), self.g_dtype, ctypes.byref(h)), 'z1_table_create')
@@ -51,10 +53,34 @@ class Table:
         numel, nch, nr = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int()
         check(lib().z1_table_info(h, ctypes.byref(numel), ctypes.byref(nch), ctypes.byref(nr)), 'z1_table_info')
         self.numel, self.nchunks = numel.value, nch.value
+        if nr.value != self.nrows:
+            raise RuntimeError(f'yoco_z1: the table reports {nr.value} rows, {self.nrows} were given')
 
     @property
     def handle(self):
         return self._h
+
+    def set_grads(self, grads):
+        """Points the rows at new gradient tensors (one per row, same sizes and dtype), enqueued on the current
+        stream; nothing is launched when the addresses are the ones the table holds."""
+        if len(grads) != self.nrows:
+            raise RuntimeError(f'yoco_z1: {len(grads)} gradients for a table of {self.nrows} rows')
+        ptrs = []
+        for g, n in zip(grads, self.sizes):
+            if _GDTYPE.get(g.dtype) != self.g_dtype or g.numel() < n:
+                raise RuntimeError('yoco_z1: a rebound gradient differs in dtype or size from its row')
+            require_gpu(g, 'yoco_z1')
+            if g.device != self.device:
+                raise RuntimeError('yoco_z1: a rebound gradient is on another device')
+            ptrs.append(g.data_ptr())
+        ptrs = tuple(ptrs)
+        if ptrs == self.grad_ptrs:
+            return
+        arr = (ctypes.c_void_p * max(1, len(ptrs)))(*ptrs)
+        with torch.cuda.device(self.device):
+            check(lib().z1_table_set_grads(self._h, ctypes.cast(arr, ctypes.c_void_p), self.nrows,
+                                           stream_handle(self.device)), 'z1_table_set_grads')
+        self.grad_ptrs = ptrs
 
     def close(self):
         h, self._h = getattr(self, '_h', None), None
@@ -70,26 +96,31 @@ class Table:
 
 
 class TableCache:
-    """Tables keyed by the addresses and sizes they describe (bounded, least recently used evicted).  A hit
-    means the same addresses and sizes, so the cached schedule is valid for whichever tensors live there now."""
+    """Tables keyed by the parameter / state addresses, sizes and gradient dtype of their rows (bounded, least
+    recently used evicted).  Gradient addresses are not part of the key: a hit whose gradients moved (autograd
+    allocates new ones after zero_grad drops them) is rebound on the stream (``Table.set_grads``), so steps neither
+    allocate nor synchronise with the device.  ``builds`` counts the tables made."""
 
     def __init__(self, capacity=8):
         self.capacity = capacity
         self._d = OrderedDict()
+        self.builds = 0
 
     def get(self, rows, device):
-        key = (str(device),) + tuple((g.data_ptr(), g.dtype, p.data_ptr() if p is not None else 0,
+        key = (str(device),) + tuple((g.dtype, p.data_ptr() if p is not None else 0,
                                       m.data_ptr() if m is not None else 0, v.data_ptr() if v is not None else 0,
                                       p16.data_ptr() if p16 is not None else 0, int(n))
                                      for g, p, m, v, p16, n in rows)
         t = self._d.get(key)
         if t is None:
             t = Table(rows, device)
+            self.builds += 1
             self._d[key] = t
             while len(self._d) > self.capacity:
                 self._d.popitem(last=False)[1].close()
         else:
             self._d.move_to_end(key)
+            t.set_grads([r[0] for r in rows])
         return t
 
     def clear(self):
@@ -98,17 +129,21 @@ class TableCache:
         self._d.clear()
 
 
-def norm_workspace(device, n=0):
-    """Workspace of the norm partials: Z1_NORM_PARTIALS doubles, or enough for a fused owner sum over n
+def norm_workspace(device, n=None):
+    """Workspace of the norm partials: Z1_NORM_PARTIALS doubles, or (n given) enough for a fused owner sum over n
     elements (its first Z1_NORM_PARTIALS doubles are what norm_clip reads)."""
-    size = Z1_NORM_PARTIALS if n <= 0 else int(lib().z1_owner_sum_workspace(int(n)))
+    size = Z1_NORM_PARTIALS if n is None else int(lib().z1_owner_sum_workspace(int(n)))
     return torch.empty(size, dtype=torch.float64, device=device)
 
 
-def grad_sumsq(table, partials):
-    require_gpu(partials, 'grad_sumsq')
+def _check_partials(partials, what):
+    require_gpu(partials, what)
     if partials.dtype != torch.float64 or partials.numel() < Z1_NORM_PARTIALS:
         raise RuntimeError('yoco_z1: norm workspace must hold Z1_NORM_PARTIALS float64')
+
+
+def grad_sumsq(table, partials):
+    _check_partials(partials, 'grad_sumsq')
     with torch.cuda.device(table.device):
         check(lib().z1_grad_sumsq(table.handle, ptr(partials), stream_handle(table.device)), 'z1_grad_sumsq')
 
@@ -152,22 +187,50 @@ def clip_factor(norm, factor=1.0, grad_norm_out=None, factor_out=None, max_norm=
               'z1_clip_factor')
 
 
+def _scalars_struct(what, sample_size=None, numer=1.0, factor=1.0, max_norm=0.0, norm_out=None,
+                    grad_norm_out=None, factor_out=None, flags_out=None, clip_log_out=None):
+    """z1_update_scalars for the given outputs (each a 1-element fp32 device tensor or None; flags_out 2 uint8)."""
+    fin, fval = _factor_args(factor)
+    if flags_out is not None:
+        require_gpu(flags_out, what)
+        if flags_out.dtype not in (torch.uint8, torch.bool) or flags_out.numel() < 2:
+            raise RuntimeError(f'{what}: flags_out must hold 2 uint8/bool')
+    return Z1UpdateScalars(_scalar(sample_size, what), f32(numer), fin, fval, f32(max_norm),
+                           _scalar(norm_out, what), _scalar(grad_norm_out, what), _scalar(factor_out, what),
+                           ptr(flags_out), _scalar(clip_log_out, what))
+
+
 def update_scalars(partials, sample_size=None, numer=1.0, factor=1.0, max_norm=0.0, norm_out=None,
                    grad_norm_out=None, factor_out=None, flags_out=None, clip_log_out=None):
     """The trainer's per-update scalar chain in one launch (include/yoco_z1.h, z1_update_scalars): optional
     sample-size factor, norm + clip chain, [finite, consistent] flags (uint8[2]) and the "clip" metric."""
     require_gpu(partials, 'update_scalars')
     dev = partials.device
-    fin, fval = _factor_args(factor)
-    if flags_out is not None:
-        require_gpu(flags_out, 'update_scalars')
-        if flags_out.dtype not in (torch.uint8, torch.bool) or flags_out.numel() < 2:
-            raise RuntimeError('update_scalars: flags_out must hold 2 uint8/bool')
-    u = Z1UpdateScalars(_scalar(sample_size, 'update_scalars'), f32(numer), fin, fval, f32(max_norm),
-                        _scalar(norm_out, 'update_scalars'), _scalar(grad_norm_out, 'update_scalars'),
-                        _scalar(factor_out, 'update_scalars'), ptr(flags_out), _scalar(clip_log_out, 'update_scalars'))
+    u = _scalars_struct('update_scalars', sample_size, numer, factor, max_norm, norm_out, grad_norm_out, factor_out,
+                        flags_out, clip_log_out)
     with torch.cuda.device(dev):
         check(lib().z1_update_scalars_run(ptr(partials), ctypes.byref(u), stream_handle(dev)), 'z1_update_scalars')
+
+
+def grad_norm_clip(table, partials, factor=1.0, norm_out=None, grad_norm_out=None, factor_out=None, max_norm=0.0):
+    """grad_sumsq + norm_clip in one call (the norm kernel, then the one-workgroup final kernel)."""
+    _check_partials(partials, 'grad_norm_clip')
+    fin, fval = _factor_args(factor)
+    with torch.cuda.device(table.device):
+        check(lib().z1_grad_norm_clip(table.handle, ptr(partials), fin, fval, _scalar(norm_out, 'grad_norm_clip'),
+                                      _scalar(grad_norm_out, 'grad_norm_clip'), _scalar(factor_out, 'grad_norm_clip'),
+                                      f32(max_norm), stream_handle(table.device)), 'z1_grad_norm_clip')
+
+
+def grad_update_scalars(table, partials, sample_size=None, numer=1.0, factor=1.0, max_norm=0.0, norm_out=None,
+                        grad_norm_out=None, factor_out=None, flags_out=None, clip_log_out=None):
+    """grad_sumsq + update_scalars in one call."""
+    _check_partials(partials, 'grad_update_scalars')
+    u = _scalars_struct('grad_update_scalars', sample_size, numer, factor, max_norm, norm_out, grad_norm_out,
+                        factor_out, flags_out, clip_log_out)
+    with torch.cuda.device(table.device):
+        check(lib().z1_grad_update_scalars(table.handle, ptr(partials), ctypes.byref(u), stream_handle(table.device)),
+              'z1_grad_update_scalars')
 
 
 def bias_corrections(beta1, beta2, step, bias_correction=1):
@@ -220,9 +283,8 @@ def bias_corrections_step(step, beta1, beta2, bc, bias_correction=1):
                                              stream_handle(step.device)), 'z1_bias_corrections_step')
 
 
-def owner_sum(contribs, out, scale, out_sum=None, partials=None):
-    """out[e] = bf16(sum_k float(contribs[k][e]) * scale), k in list order.  contribs: bf16 tensors (or raw
-    device addresses as ints) of out.numel() elements each; out may be one of them."""
+def _owner_sum_args(contribs, out, out_sum, workspace):
+    """Checked (host pointer array, world) for an owner-sum call."""
     require_gpu(out, 'owner_sum')
     if out.dtype != torch.bfloat16 or not out.is_contiguous():
         raise RuntimeError('yoco_z1: owner_sum output must be a contiguous bf16 tensor')
@@ -242,16 +304,38 @@ def owner_sum(contribs, out, scale, out_sum=None, partials=None):
         require_gpu(out_sum, 'owner_sum')
         if out_sum.dtype != torch.float32 or not out_sum.is_contiguous() or out_sum.numel() != out.numel():
             raise RuntimeError('yoco_z1: owner_sum out_sum must be a contiguous fp32 tensor like out')
-    if partials is not None:
-        require_gpu(partials, 'owner_sum')
+    if workspace is not None:
+        require_gpu(workspace, 'owner_sum')
         need = int(lib().z1_owner_sum_workspace(out.numel()))
-        if partials.dtype != torch.float64 or partials.numel() < need:
+        if workspace.dtype != torch.float64 or workspace.numel() < need or not workspace.is_contiguous():
             raise RuntimeError(f'yoco_z1: the fused-norm workspace must hold {need} float64 '
                                f'(ops.norm_workspace(device, n))')
-    arr = (ctypes.c_void_p * world)(*addrs)
+    return (ctypes.c_void_p * world)(*addrs), world
+
+
+def owner_sum(contribs, out, scale, out_sum=None, partials=None):
+    """out[e] = bf16(sum_k float(contribs[k][e]) * scale), k in list order.  contribs: bf16 tensors (or raw
+    device addresses as ints) of out.numel() elements each; out may be one of them."""
+    arr, world = _owner_sum_args(contribs, out, out_sum, partials)
     with torch.cuda.device(out.device):
         check(lib().z1_owner_sum_bf16(ctypes.cast(arr, ctypes.c_void_p), world, out.numel(), f32(scale), ptr(out),
                                       ptr(out_sum), ptr(partials), stream_handle(out.device)), 'z1_owner_sum_bf16')
+
+
+def owner_sum_update(contribs, out, scale, workspace, out_sum=None, sample_size=None, numer=1.0, factor=1.0,
+                     max_norm=0.0, norm_out=None, grad_norm_out=None, factor_out=None, flags_out=None,
+                     clip_log_out=None):
+    """owner_sum with the fused norm, then the update_scalars chain on its partials, in one call
+    (z1_owner_sum_update).  workspace: ops.norm_workspace(device, out.numel())."""
+    if workspace is None:
+        raise RuntimeError('yoco_z1: owner_sum_update needs its workspace')
+    arr, world = _owner_sum_args(contribs, out, out_sum, workspace)
+    u = _scalars_struct('owner_sum_update', sample_size, numer, factor, max_norm, norm_out, grad_norm_out,
+                        factor_out, flags_out, clip_log_out)
+    with torch.cuda.device(out.device):
+        check(lib().z1_owner_sum_update(ctypes.cast(arr, ctypes.c_void_p), world, out.numel(), f32(scale), ptr(out),
+                                        ptr(out_sum), ptr(workspace), ctypes.byref(u), stream_handle(out.device)),
+              'z1_owner_sum_update')
 
 
 def owner_sum_raw(addrs, n, out_addr, scale, device):

@@ -6,9 +6,9 @@ HBM layout (one allocation per stream, every tensor's slice starting on a ``alig
     p    fp32 [N]   master weights            m    fp32 [N]   exp_avg
     v    fp32 [N]   exp_avg_sq                g    fp32 or bf16 [N]   owner gradient (the reduced average)
     p16  bf16 [N]   the parameter copy the model reads
-plus a device-resident offset table (one row per tensor) built once.  One optimizer update is three launches:
-sum of squares (fixed-order partials) -> final reduction + clip factor -> Adam + BF16 over the table.  With
-owner-side contributions (``reduce_grads``) the sum of squares is fused into the owner sum.
+plus a device-resident offset table (one row per tensor) built once.  One optimizer update is three launches: the
+norm (fixed-order partials) -> its final reduction + the clip chain (one workgroup) -> Adam + BF16 over the table.
+With owner-side contributions (``reduce_grads`` / ``reduce_clip``) the norm is fused into the owner sum.
 """
 import math
 
@@ -102,7 +102,7 @@ class Zero1ShardOptimizer:
         self._multiply_factor = 1.0
         self._needs_sync = False
         dev = shard.device
-        self._partials = ops.norm_workspace(dev, shard.total if shard.g.dtype == torch.bfloat16 else 0)
+        self._partials = ops.norm_workspace(dev, shard.total if shard.g.dtype == torch.bfloat16 else None)
         self._factor = torch.ones(1, dtype=torch.float32, device=dev)
         self._norm = torch.zeros(1, dtype=torch.float32, device=dev)
         self._partials_ready = False
@@ -145,23 +145,53 @@ class Zero1ShardOptimizer:
         # the fused partials cover the whole flat buffer; with alignment gaps the norm is taken over the table
         self._partials_ready = self.shard.total == self.shard.numel
 
+    def reduce_clip(self, contribs, max_norm, scale=None, sample_size=None, numer=1.0, flags_out=None,
+                    clip_log_out=None):
+        """reduce_grads + (the trainer's sample-size factor +) clip_grad_norm(max_norm) as one fused pass: the
+        owner sum with the norm fused in, then the scalar chain on its partials (the owner's part of
+        yoco/tasks/trainer_nosync.py:268-286).  Returns grad_norm (0-d device tensor), no host sync."""
+        if self.shard.g.dtype != torch.bfloat16:
+            raise RuntimeError('yoco_z1: reduce_clip needs a bf16 gradient shard')
+        world = len(contribs)
+        sc = 1.0 / world if scale is None else scale
+        factor, out = self._clip_factor_args()
+        grad_norm = torch.empty(1, dtype=torch.float32, device=self.shard.device)
+        mn = float(max_norm)
+        kw = dict(sample_size=sample_size, numer=numer, factor=factor, max_norm=mn if mn > 0.0 else 0.0,
+                  norm_out=self._norm, grad_norm_out=grad_norm, factor_out=out, flags_out=flags_out,
+                  clip_log_out=clip_log_out)
+        with record_function('reduce-grads'):        # the reference's profiler region (trainer_nosync.py:268)
+            if self.shard.total == self.shard.numel:
+                ops.owner_sum_update(contribs, self.shard.g, sc, self._partials, **kw)
+            else:       # alignment gaps: the norm is taken over the table's rows, not the whole flat buffer
+                ops.owner_sum(contribs, self.shard.g, sc)
+                ops.grad_update_scalars(self.shard.table, self._partials, **kw)
+        self._partials_ready = False
+        self._multiply_factor = out
+        self._needs_sync = False
+        return grad_norm.view(())
+
     def clip_grad_norm(self, max_norm, aggregate_norm_fn=None):
         """zero1_fast.py:139-162 for one owner.  Returns grad_norm as a 0-d fp32 device tensor, no host sync."""
-        if not self._partials_ready:
-            ops.grad_sumsq(self.shard.table, self._partials)
-        self._partials_ready = False
         factor, out = self._clip_factor_args()
         grad_norm = torch.empty(1, dtype=torch.float32, device=self.shard.device)
         mn = float(max_norm)
         if aggregate_norm_fn is None:
-            ops.norm_clip(self._partials, factor=factor, norm_out=self._norm, grad_norm_out=grad_norm,
-                          factor_out=out, max_norm=mn if mn > 0.0 else 0.0)
+            clip = dict(factor=factor, norm_out=self._norm, grad_norm_out=grad_norm, factor_out=out,
+                        max_norm=mn if mn > 0.0 else 0.0)
+            if self._partials_ready:
+                ops.norm_clip(self._partials, **clip)
+            else:
+                ops.grad_norm_clip(self.shard.table, self._partials, **clip)
         else:
+            if not self._partials_ready:
+                ops.grad_sumsq(self.shard.table, self._partials)
             ops.norm_clip(self._partials, factor=1.0, norm_out=self._norm)
             norm = (self._norm.float() ** 2).sqrt()
             norm = aggregate_norm_fn(norm).reshape(1).to(torch.float32)
             ops.clip_factor(norm, factor=factor, grad_norm_out=grad_norm, factor_out=out,
                             max_norm=mn if mn > 0.0 else 0.0)
+        self._partials_ready = False
         self._multiply_factor = out
         self._needs_sync = False
         return grad_norm.view(())
@@ -170,15 +200,17 @@ class Zero1ShardOptimizer:
         """multiply_grads(numer / where(sample_size > 0, sample_size, 1)) + clip_grad_norm(max_norm) in one launch,
         also writing the [finite, consistent] flags and the "clip" metric (yoco/tasks/trainer_nosync.py:273-286,
         :194-197).  sample_size: 1-element fp32 device tensor or None.  Returns grad_norm (0-d device tensor)."""
-        if not self._partials_ready:
-            ops.grad_sumsq(self.shard.table, self._partials)
-        self._partials_ready = False
         factor, out = self._clip_factor_args()
         grad_norm = torch.empty(1, dtype=torch.float32, device=self.shard.device)
         mn = float(max_norm)
-        ops.update_scalars(self._partials, sample_size=sample_size, numer=numer, factor=factor,
-                           max_norm=mn if mn > 0.0 else 0.0, norm_out=self._norm, grad_norm_out=grad_norm,
-                           factor_out=out, flags_out=flags_out, clip_log_out=clip_log_out)
+        kw = dict(sample_size=sample_size, numer=numer, factor=factor, max_norm=mn if mn > 0.0 else 0.0,
+                  norm_out=self._norm, grad_norm_out=grad_norm, factor_out=out, flags_out=flags_out,
+                  clip_log_out=clip_log_out)
+        if self._partials_ready:
+            ops.update_scalars(self._partials, **kw)
+        else:
+            ops.grad_update_scalars(self.shard.table, self._partials, **kw)
+        self._partials_ready = False
         self._multiply_factor = out
         self._needs_sync = False
         return grad_norm.view(())

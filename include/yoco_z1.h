@@ -64,8 +64,18 @@ int z1_table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table** ou
  * table complete).  Not during stream capture; a captured graph whose launches use the table must not be replayed
  * after it. */
 int z1_table_destroy(z1_table* table);
-/* Total elements and chunk count of a table (host-side values). */
+/* Total elements, chunk count and row count of a table (host-side values).  nrows is the count given to
+ * z1_table_create, empty rows included: the row indices z1_adam_cast_rows and z1_table_set_grads take. */
 int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* nrows);
+
+/* Points the table's rows at new gradient tensors of the same sizes and dtype: g is a HOST array of nrows device
+ * pointers, one per row given to z1_table_create (entries of empty rows are ignored and may be NULL).  Enqueued on
+ * the stream like a launch (no allocation, no host synchronisation): launches enqueued after it read the new
+ * gradients.  For callers whose gradient tensors are reallocated between steps while the parameters and optimizer
+ * state stay put (the reference's zero_grad drops every gradient, yoco/tasks/zero1_fast.py:238-244), so that one
+ * table made at set-up serves every step.  Rows whose new gradient is not aligned for the vector path take the
+ * element-wise path. */
+int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* stream);
 
 /* Owner-side sum (replaces the Triton kernel _sum_slots, yoco/models/decoder/ce_reduce.py:59-74, launched by
  * CEReduce._sum :178-183):
@@ -76,13 +86,20 @@ int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* 
  * first Z1_NORM_PARTIALS doubles are ready for z1_norm_clip when the call's work completes. */
 int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
                       float* out_sum, double* sumsq_partials, void* stream);
-/* Doubles the fused-norm workspace of z1_owner_sum_bf16 must hold for n elements (negative: error code). */
+/* Doubles the fused-norm workspace of z1_owner_sum_bf16 / z1_owner_sum_update must hold for n elements
+ * (negative: error code). */
 int64_t z1_owner_sum_workspace(int64_t n);
 
 /* Multi-tensor sum of squares of the table's gradients (the norm of fairseq utils.clip_grad_norm_ ->
  * apex multi_tensor_l2norm, called at yoco/tasks/zero1_fast.py:150,157): per-workgroup FP64 partials over a fixed
  * decomposition into `partials` (Z1_NORM_PARTIALS doubles), no atomics. */
 int z1_grad_sumsq(const z1_table* table, double* partials, void* stream);
+
+/* z1_grad_sumsq then z1_norm_clip in one call (the norm kernel and the one-workgroup final kernel, the same bits):
+ * the norm + clip of yoco/tasks/zero1_fast.py:150-160 (fairseq utils.clip_grad_norm_ -> apex multi_tensor_l2norm,
+ * then the torch scalar ops). */
+int z1_grad_norm_clip(const z1_table* table, double* partials, const float* factor_in, float factor_value,
+                      float* norm_out, float* grad_norm_out, float* factor_out, float max_norm, void* stream);
 
 /* Fixed-order final reduction of the partials and the clip chain of yoco/tasks/zero1_fast.py:150-160 on device:
  *   n_r = fp32(sqrt(sum)); sq = n_r*n_r; norm = sqrt(sq); grad_norm = factor*norm;
@@ -110,6 +127,17 @@ typedef struct z1_update_scalars {
     float* clip_log_out;       /* 100 if grad_norm > max_norm else 0 (written when max_norm > 0) */
 } z1_update_scalars;
 int z1_update_scalars_run(const double* partials, const z1_update_scalars* u, void* stream);
+
+/* z1_grad_sumsq then z1_update_scalars_run in one call. */
+int z1_grad_update_scalars(const z1_table* table, double* partials, const z1_update_scalars* u, void* stream);
+
+/* The owner sum with the norm fused in, then the z1_update_scalars chain, in one call: the owner sum of
+ * yoco/models/decoder/ce_reduce.py:59-74, the norm and clip of yoco/tasks/zero1_fast.py:150-160 and optionally the
+ * trainer's scalars of yoco/tasks/trainer_nosync.py:273-286 -- z1_owner_sum_bf16 followed by z1_update_scalars_run
+ * on its partials (the same launches and bits).  workspace: z1_owner_sum_workspace(n) doubles; its first
+ * Z1_NORM_PARTIALS hold the partials afterwards. */
+int z1_owner_sum_update(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                        float* out_sum, double* workspace, const z1_update_scalars* u, void* stream);
 
 /* The clip chain entered at `norm` (device fp32), for callers that post-process the norm (aggregate_norm_fn,
  * yoco/tasks/zero1_fast.py:153-160): grad_norm = factor*norm; clip as above.  Factor arguments as above. */

@@ -1,12 +1,15 @@
 /* Plain-C, torch-free consumer of include/yoco_z1.h on the GPU (what a binding from another language does):
  * device buffers from hipMalloc, every call through the C ABI on the null stream, results checked against the CPU
  * oracle's C functions (oracle/z1_oracle.c, test infrastructure) at the parity bars of the Python suite:
- *   1. a 4-row table (tails, a row below one chunk, 64-element row alignment): sum of squares -> norm + clip
- *      -> Adam + BF16 copy with the device factor; norm within 1e-6 of the exact one, the clip chain bit-exact
- *      from the GPU's norm, p / m / v / BF16 bit-exact given the GPU's factor;
- *      A second step runs as two launches over row ranges (z1_adam_cast_rows), again bit-exact;
+ *   1. a 5-row table (tails, a row below one chunk, an empty row, 64-element row alignment): sum of squares ->
+ *      norm + clip -> Adam + BF16 copy with the device factor; norm within 1e-6 of the exact one, the clip chain
+ *      bit-exact from the GPU's norm, p / m / v / BF16 bit-exact given the GPU's factor; the one-call
+ *      z1_grad_norm_clip (three calls in a row) gives the same bits as the two calls.  A second step, on new
+ *      gradients bound with z1_table_set_grads (one of them misaligned), runs as two launches over row ranges
+ *      bounded by z1_table_info's row count (empty row included), again bit-exact;
  *   2. the owner sum of 8 BF16 contributions with the fused norm: average and FP32 sum bit-exact, norm within
- *      1e-6 of the average's exact norm;
+ *      1e-6 of the average's exact norm; z1_owner_sum_update (with the clip chain, twice, then on a shorter
+ *      input with the same workspace) gives the same bits as z1_owner_sum_bf16 + z1_norm_clip;
  *   3. the embedding gradient (workspace query, ids with repeats, out-of-range ids and padding, x 1/8 after) at
  *      5000 rows (aten's sort-path order) and 1000 rows (its order for few indices): bit-exact.
  * Built by __graft_entry__.build() with gcc, linked against libyoco_z1.so, the oracle and the HIP runtime, twice:
@@ -84,8 +87,8 @@ static uint32_t bits(float x) {
 static int same_f32(const float* a, const float* b, int64_t n) { return memcmp(a, b, (size_t)n * 4) == 0; }
 
 static int table_update(void) {
-    enum { R = 4 };
-    const int64_t sizes[R] = {70001, 256 * 37, 100, 4096 * 3 + 7};
+    enum { R = 5 };
+    const int64_t sizes[R] = {70001, 256 * 37, 0, 100, 4096 * 3 + 7};
     int64_t off[R], total = 0;
     for (int i = 0; i < R; ++i) {
         off[i] = total;
@@ -100,15 +103,16 @@ static int table_update(void) {
         hm[i] = normal(1e-4);
         hv[i] = fabsf(normal(1e-8));
     }
-    float *dg, *dp, *dm, *dv, *ds;
+    float *dg, *dg2, *dp, *dm, *dv, *ds;
     uint16_t* d16;
     double* dpart;
     HIP_OK(hipMalloc((void**)&dg, total * 4));
+    HIP_OK(hipMalloc((void**)&dg2, (total + 1) * 4));
     HIP_OK(hipMalloc((void**)&dp, total * 4));
     HIP_OK(hipMalloc((void**)&dm, total * 4));
     HIP_OK(hipMalloc((void**)&dv, total * 4));
     HIP_OK(hipMalloc((void**)&d16, total * 2));
-    HIP_OK(hipMalloc((void**)&ds, 3 * 4));
+    HIP_OK(hipMalloc((void**)&ds, 6 * 4));
     HIP_OK(hipMalloc((void**)&dpart, Z1_NORM_PARTIALS * 8));
     HIP_OK(hipMemcpy(dg, hg, total * 4, hipMemcpyHostToDevice));
     HIP_OK(hipMemcpy(dp, hp, total * 4, hipMemcpyHostToDevice));
@@ -129,7 +133,7 @@ static int table_update(void) {
     int64_t numel = 0, nch = 0;
     int nr = 0;
     Z1_OK_(z1_table_info(t, &numel, &nch, &nr));
-    EXPECT(nr == R && numel == sizes[0] + sizes[1] + sizes[2] + sizes[3]);
+    EXPECT(nr == R && numel == sizes[0] + sizes[1] + sizes[2] + sizes[3] + sizes[4]);   /* the empty row counts */
 
     const float lr = 3e-4f, b1 = 0.9f, b2 = 0.95f, eps = 1e-8f, wd = 0.1f, max_norm = 1.0f;
     const int64_t step = 1000;
@@ -137,6 +141,16 @@ static int table_update(void) {
     oracle_bias_corrections(0.9, 0.95, step, 1, bc);
     Z1_OK_(z1_grad_sumsq(t, dpart, NULL));
     Z1_OK_(z1_norm_clip(dpart, NULL, 1.0f, ds + 0, ds + 1, ds + 2, max_norm, NULL));
+    for (int rep = 0; rep < 3; ++rep) {           /* the one-call form: same bits, every call */
+        float one[3];
+        HIP_OK(hipMemset(ds + 3, 0, 12));
+        Z1_OK_(z1_grad_norm_clip(t, dpart, NULL, 1.0f, ds + 3, ds + 4, ds + 5, max_norm, NULL));
+        HIP_OK(hipDeviceSynchronize());
+        float two[3];
+        HIP_OK(hipMemcpy(two, ds, 12, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(one, ds + 3, 12, hipMemcpyDeviceToHost));
+        EXPECT(bits(one[0]) == bits(two[0]) && bits(one[1]) == bits(two[1]) && bits(one[2]) == bits(two[2]));
+    }
     Z1_OK_(z1_adam_cast(t, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL));
     HIP_OK(hipDeviceSynchronize());
     float sc[3];
@@ -161,13 +175,25 @@ static int table_update(void) {
         EXPECT(same_f32(op + o, hp + o, n) && same_f32(om + o, hm + o, n) && same_f32(ov + o, hv + o, n));
         EXPECT(memcmp(o16 + o, h16 + o, (size_t)n * 2) == 0);
     }
-    /* step 1001 from that state as two launches over row ranges, the factor 0.75 on the host side */
+    /* step 1001 from that state on new gradients (bound with z1_table_set_grads; row 3 one element off the vector
+     * alignment) as two launches over row ranges up to z1_table_info's row count, the factor 0.75 */
+    int64_t off2[R];
+    const void* g2[R];
+    for (int i = 0; i < R; ++i) {
+        off2[i] = off[i] + (i == 3);
+        g2[i] = i == 2 ? NULL : (const void*)(dg2 + off2[i]);  /* the empty row's entry is ignored */
+    }
+    for (int64_t i = 0; i < total; ++i) hg[i] = normal(1e-2);
+    for (int i = 0; i < R; ++i)
+        if (sizes[i]) HIP_OK(hipMemcpy(dg2 + off2[i], hg + off[i], sizes[i] * 4, hipMemcpyHostToDevice));
+    EXPECT(z1_table_set_grads(t, g2, R - 1, NULL) == Z1_E_SIZE);
+    Z1_OK_(z1_table_set_grads(t, g2, R, NULL));
     oracle_bias_corrections(0.9, 0.95, step + 1, 1, bc);
     const float f2 = 0.75f;
     HIP_OK(hipMemcpy(ds + 2, &f2, 4, hipMemcpyHostToDevice));
-    EXPECT(z1_adam_cast_rows(t, 3, 5, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL) == Z1_E_SIZE);
+    EXPECT(z1_adam_cast_rows(t, 3, nr + 1, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL) == Z1_E_SIZE);
     Z1_OK_(z1_adam_cast_rows(t, 0, 1, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL));
-    Z1_OK_(z1_adam_cast_rows(t, 1, R, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL));
+    Z1_OK_(z1_adam_cast_rows(t, 1, nr, ds + 2, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL));
     HIP_OK(hipDeviceSynchronize());
     HIP_OK(hipMemcpy(op, dp, total * 4, hipMemcpyDeviceToHost));
     HIP_OK(hipMemcpy(om, dm, total * 4, hipMemcpyDeviceToHost));
@@ -181,6 +207,7 @@ static int table_update(void) {
     }
     Z1_OK_(z1_table_destroy(t));
     HIP_OK(hipFree(dg));
+    HIP_OK(hipFree(dg2));
     HIP_OK(hipFree(dp));
     HIP_OK(hipFree(dm));
     HIP_OK(hipFree(dv));
@@ -223,6 +250,36 @@ static int owner_sum(void) {
     EXPECT(same_f32(hsum, esum, n));
     const double exact = sqrt(oracle_sumsq_bf16(eavg, n));
     EXPECT(fabs((double)nrm - exact) <= 1e-6 * exact);
+    /* z1_owner_sum_update against z1_owner_sum_bf16 + z1_norm_clip: twice on n, then on a shorter input with the
+     * same workspace */
+    float* dsc;
+    HIP_OK(hipMalloc((void**)&dsc, 6 * 4));
+    const int64_t lens[3] = {n, n, 4099};
+    for (int rep = 0; rep < 3; ++rep) {
+        const int64_t m = lens[rep];
+        const float fac = rep == 1 ? 3.0f : 0.5f;
+        Z1_OK_(z1_owner_sum_bf16((const uint16_t* const*)dc, W, m, 0.125f, davg, NULL, dws, NULL));
+        Z1_OK_(z1_norm_clip(dws, NULL, fac, dsc + 0, dsc + 1, dsc + 2, 1.0f, NULL));
+        HIP_OK(hipDeviceSynchronize());
+        HIP_OK(hipMemcpy(eavg, davg, m * 2, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemset(davg, 0, n * 2));
+        z1_update_scalars u;
+        memset(&u, 0, sizeof(u));
+        u.numer = 1.0f;
+        u.factor_value = fac;
+        u.max_norm = 1.0f;
+        u.norm_out = dsc + 3;
+        u.grad_norm_out = dsc + 4;
+        u.factor_out = dsc + 5;
+        Z1_OK_(z1_owner_sum_update((const uint16_t* const*)dc, W, m, 0.125f, davg, NULL, dws, &u, NULL));
+        HIP_OK(hipDeviceSynchronize());
+        float sc[6];
+        HIP_OK(hipMemcpy(sc, dsc, 24, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(havg, davg, m * 2, hipMemcpyDeviceToHost));
+        EXPECT(memcmp(havg, eavg, (size_t)m * 2) == 0);
+        EXPECT(bits(sc[0]) == bits(sc[3]) && bits(sc[1]) == bits(sc[4]) && bits(sc[2]) == bits(sc[5]));
+    }
+    HIP_OK(hipFree(dsc));
     for (int k = 0; k < W; ++k) {
         HIP_OK(hipFree(dc[k]));
         free(hc[k]);

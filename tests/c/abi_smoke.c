@@ -25,12 +25,15 @@ int main(void) {
         bad |= z1_table_create(r, 2, Z1_F32, &t) != Z1_E_SIZE;
         bad |= t != 0;
     }
-    bad |= z1_owner_sum_workspace(513) != Z1_NORM_PARTIALS + 2;
+    bad |= z1_owner_sum_workspace(513) != Z1_NORM_PARTIALS + 2;       /* the partials, then one per chunk */
+    bad |= z1_grad_norm_clip(0, 0, 0, 1.f, 0, 0, 0, 1.f, 0) != Z1_E_NULL;
+    bad |= z1_table_set_grads(0, 0, 0, 0) != Z1_E_NULL;
     bad |= z1_adam_cast(0, 0, 0.f, 0.f, 0.f, 0.f, 1.f, 1.f, 0.f, 1, 0) != Z1_E_NULL;
     bad |= strlen(z1_strerror(Z1_E_WORKSPACE)) == 0;
     z1_update_scalars u;
     memset(&u, 0, sizeof(u));
     bad |= z1_update_scalars_run(0, &u, 0) != Z1_E_NULL;
+    bad |= z1_grad_update_scalars(0, 0, &u, 0) != Z1_E_NULL;
     bad |= z1_embedding_backward_workspace(-1, 8, 10) != Z1_E_SIZE;
     bad |= z1_embedding_backward_workspace(16, 0, 10) != Z1_E_SIZE;
     bad |= z1_embedding_backward_workspace(16, (1 << 24) + 1, 10) != Z1_E_SIZE;

@@ -68,6 +68,16 @@ def test_argument_errors_without_device_work(pkg):
     assert L.z1_table_destroy(None) == 0
     assert L.z1_owner_sum_workspace(-1) == -2
     assert [L.z1_owner_sum_workspace(n) for n in (0, 1, 512, 513)] == [2048, 2049, 2049, 2050]
+    assert L.z1_grad_norm_clip(None, None, None, 1.0, None, None, None, 1.0, None) == -1
+    assert L.z1_grad_update_scalars(None, None, None, None) == -1
+    assert L.z1_table_set_grads(None, None, 0, None) == -1
+    u = _lib.Z1UpdateScalars()
+    assert L.z1_owner_sum_update(ctypes.cast(arr, ctypes.c_void_p), 1, 10, 1.0, ctypes.c_void_p(32), None, None,
+                                 ctypes.byref(u), None) == -1                      # no workspace
+    assert L.z1_owner_sum_update(ctypes.cast(arr, ctypes.c_void_p), 1, 10, 1.0, ctypes.c_void_p(32), None,
+                                 ctypes.c_void_p(64), None, None) == -1            # no scalar outputs struct
+    assert L.z1_owner_sum_update(ctypes.cast(arr, ctypes.c_void_p), 0, 10, 1.0, ctypes.c_void_p(32), None,
+                                 ctypes.c_void_p(64), ctypes.byref(u), None) == -4
     assert L.z1_table_info(None, None, None, None) == -1
     for code in (0, -1, -2, -3, -4, -5, -6, -7, -99):
         assert L.z1_strerror(code)
