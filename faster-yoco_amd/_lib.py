@@ -18,6 +18,7 @@ Z1_F32 = 0
 Z1_BF16 = 1
 Z1_MAX_WORLD = 16
 Z1_NORM_PARTIALS = 2048
+Z1_NOALLOC_MAX_N = 1 << 29
 
 _P = ctypes.c_void_p
 _I = ctypes.c_int
@@ -45,6 +46,7 @@ SIGNATURES = {
     'z1_owner_sum_bf16': ([_P, _I, _I64, _F, _P, _P, _P, _P], _I),
     'z1_owner_sum_workspace': ([_I64], _I64),
     'z1_owner_sum_update': ([_P, _I, _I64, _F, _P, _P, _P, ctypes.POINTER(Z1UpdateScalars), _P], _I),
+    'z1_owner_sum_update_noalloc': ([_P, _I, _I64, _F, _P, _P, ctypes.POINTER(Z1UpdateScalars), _P], _I),
     'z1_table_set_grads': ([_P, _P, _I, _P], _I),
     'z1_grad_sumsq': ([_P, _P, _P], _I),
     'z1_grad_norm_clip': ([_P, _P, _P, _F, _P, _P, _P, _F, _P], _I),

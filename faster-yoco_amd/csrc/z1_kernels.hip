@@ -645,6 +645,32 @@ inline int launch_status() {
 
 }  // namespace
 
+// Scratch of z1_owner_sum_update_noalloc: the norm's Z1_NORM_PARTIALS partials, then one per-wave partial per
+// owner-sum chunk, for up to Z1_NOALLOC_MAX_N elements (8.0 MiB; every device the library runs on holds its own copy
+// until the process ends).  Host code never passes this name to a kernel: in host code it is a stand-in, not a
+// device address.  The address of a device's copy comes from hipGetSymbolAddress, once per device.
+constexpr int64_t kNoallocDoubles = Z1_NORM_PARTIALS + Z1_NOALLOC_MAX_N / kSumChunk;
+static_assert(Z1_NOALLOC_MAX_N % kSumChunk == 0, "the no-allocation maximum is a whole number of chunks");
+static __device__ __align__(256) double scratch[kNoallocDoubles];
+
+namespace {
+double* g_scratch_ptr[kMaxDevices];   // device address of `scratch` per device (nullptr: not looked up yet)
+
+// The current device's copy of `scratch`, looked up on the first call on that device with the device current.
+int scratch_address(int dev, double** out) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        if (!ptr) return Z1_E_NULL;
+        g_scratch_ptr[dev] = static_cast<double*>(ptr);
+    }
+    *out = g_scratch_ptr[dev];
+    return Z1_OK;
+}
+}  // namespace
+
 struct z1_table {
     Row* rows;            // device, one allocation: the non-empty rows, then nchunks int32 chunk -> row entries
     int32_t* chunk_row;
@@ -1021,6 +1047,22 @@ int z1_owner_sum_update(const uint16_t* const* contrib, int world, int64_t n, fl
     return owner_sum(contrib, world, n, scale, out_avg, out_sum, workspace, u, stream);
 }
 
+int z1_owner_sum_update_noalloc(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                                float* out_sum, const z1_update_scalars* u, void* stream) {
+    if (!u) return Z1_E_NULL;
+    if (n < 0) return Z1_E_SIZE;
+    if (n > Z1_NOALLOC_MAX_N) return Z1_E_NOALLOC_MAX;
+    int dev = 0;
+    int rc = current_device(&dev);
+    if (rc) return rc;
+    double* ws = nullptr;
+    rc = scratch_address(dev, &ws);
+    if (rc) return rc;
+    // every scratch slot this call reads is written by it first (the per-wave partials by the owner sum, the
+    // Z1_NORM_PARTIALS partials by their reduction), so nothing needs clearing between calls
+    return owner_sum(contrib, world, n, scale, out_avg, out_sum, ws, u, stream);
+}
+
 int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n, void* stream) {
     if (n < 0) return Z1_E_SIZE;
     if (n == 0) return Z1_OK;
@@ -1061,6 +1103,7 @@ const char* z1_strerror(int code) {
         case Z1_E_MODE: return "Adam mode must be 0 or 1";
         case Z1_E_WORKSPACE: return "workspace too small";
         case Z1_E_DEVICE: return "table used on another device than it was created on";
+        case Z1_E_NOALLOC_MAX: return "more than Z1_NOALLOC_MAX_N elements for the no-allocation entry point";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

@@ -35,12 +35,14 @@ enum {
     Z1_E_MODE = -5,        /* Adam mode other than 0 or 1 */
     Z1_E_WORKSPACE = -6,   /* workspace too small */
     Z1_E_DEVICE = -7,      /* table used on a device other than the one it was created on */
+    Z1_E_NOALLOC_MAX = -8, /* input larger than the no-allocation entry point's fixed scratch */
 };
 
 enum { Z1_F32 = 0, Z1_BF16 = 1 };           /* gradient dtype codes */
 
 #define Z1_MAX_WORLD 16                      /* most contributions one owner-sum call takes */
 #define Z1_NORM_PARTIALS 2048                /* doubles in the norm workspace (fixed: the reduction order) */
+#define Z1_NOALLOC_MAX_N (1ll << 29)         /* most elements z1_owner_sum_update_noalloc takes */
 
 /* One row of the tensor-offset table.  g is float* (Z1_F32) or uint16_t* bfloat16 bits (Z1_BF16).  For the norm
  * only g and n are read; p, m, v may be NULL there.  p16 may be NULL (no BF16 copy for that tensor). */
@@ -138,6 +140,17 @@ int z1_grad_update_scalars(const z1_table* table, double* partials, const z1_upd
  * Z1_NORM_PARTIALS hold the partials afterwards. */
 int z1_owner_sum_update(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
                         float* out_sum, double* workspace, const z1_update_scalars* u, void* stream);
+
+/* z1_owner_sum_update with its workspace in the library's own fixed device scratch (a static device array of
+ * 8.0 MiB per device, held until the process ends): no allocation of any kind, so callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc -- can run the owner sum, norm
+ * and clip chain.  No counterpart in the reference.  n is at most Z1_NOALLOC_MAX_N (Z1_E_NOALLOC_MAX beyond; the
+ * largest YOCO-3B owner shard is 443,357,184).  Every call on one device shares that device's scratch: calls that
+ * overlap in time on one device (several streams, several threads) race.  Each call writes every scratch slot it
+ * reads, so nothing carries over from the previous call.  The first call on a device looks up the scratch's
+ * address there (hipGetSymbolAddress). */
+int z1_owner_sum_update_noalloc(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                                float* out_sum, const z1_update_scalars* u, void* stream);
 
 /* The clip chain entered at `norm` (device fp32), for callers that post-process the norm (aggregate_norm_fn,
  * yoco/tasks/zero1_fast.py:153-160): grad_norm = factor*norm; clip as above.  Factor arguments as above. */
