@@ -8,7 +8,9 @@
 // the indices in chunks of 16: per chunk and id an fp32 sum in position order, rounded to bf16 and added to the
 // bf16 row (emb_rows_kernel<true>; no heavy passes).  padding_idx rows and ids outside [0, V) contribute nothing.
 //
-//   1. keys[i] = id_i (or V when out of range), vals[i] = i;  2. stable radix sort (hipCUB / rocPRIM);
+//   1. keys[i] = id_i (or V when out of range), vals[i] = i;  2. stable sort by key: hipCUB's radix sort, or,
+//      while the stream is being captured into a HIP graph, rocPRIM's merge sort, which clears nothing with
+//      memsets (the radix sort does; both are stable, so the order is the same: 0.136 vs 0.142 ms per call);
 //   3. row_lo[t] = start of id t's run in the sorted keys (one binary search per t, all in parallel);
 //   4. one wave per output row t writes the row's sums -- or zeros -- exactly once, 8 bf16 columns per lane, with
 //      nontemporal stores (aten zero-fills the whole table and then scatters into it; here every row of the table
@@ -21,6 +23,7 @@
 //      milliseconds.
 #include <hip/hip_runtime.h>
 #include <hipcub/hipcub.hpp>
+#include <rocprim/device/device_merge_sort.hpp>
 
 #include <stdint.h>
 
@@ -395,11 +398,26 @@ __global__ __launch_bounds__(kWave * kChainWaves) void emb_heavy_chain_kernel(co
     }
 }
 
+// Stable sort of the (key, position) pairs by key: equal keys keep their position order, which is aten's order.
+// end_bit bounds the radix sort's passes (keys are at most V); merge selects the sort that records no memset.
+hipError_t sort_pairs(void* temp, size_t& bytes, const uint32_t* keys, uint32_t* skeys, const int32_t* vals,
+                      int32_t* svals, int64_t R, int end_bit, bool merge, hipStream_t st) {
+    if (merge)
+        return rocprim::merge_sort(temp, bytes, keys, skeys, vals, svals, (size_t)R, rocprim::less<uint32_t>(), st);
+    return hipcub::DeviceRadixSort::SortPairs(temp, bytes, keys, skeys, vals, svals, (int)R, 0, end_bit, st);
+}
+
 size_t sort_temp_bytes(int64_t R) {
-    size_t bytes = 0;
-    (void)hipcub::DeviceRadixSort::SortPairs(nullptr, bytes, (const uint32_t*)nullptr, (uint32_t*)nullptr,
-                                             (const int32_t*)nullptr, (int32_t*)nullptr, (int)R, 0, 32);
-    return bytes;
+    size_t radix = 0, merge = 0;
+    (void)sort_pairs(nullptr, radix, nullptr, nullptr, nullptr, nullptr, R, 32, false, 0);
+    (void)sort_pairs(nullptr, merge, nullptr, nullptr, nullptr, nullptr, R, 32, true, 0);
+    return radix > merge ? radix : merge;
+}
+
+// Whether work enqueued on `st` is being captured into a graph (an error reads as not capturing).
+bool capturing(hipStream_t st) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(st, &status) == hipSuccess && status != hipStreamCaptureStatusNone;
 }
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -481,7 +499,7 @@ int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, i
         size_t tb = w.temp_bytes;
         int end_bit = 1;
         while (end_bit < 32 && ((uint64_t)V >> end_bit) != 0) ++end_bit;   // keys are <= V
-        e = hipcub::DeviceRadixSort::SortPairs(w.temp, tb, w.keys, w.skeys, w.vals, w.svals, (int)R, 0, end_bit, st);
+        e = sort_pairs(w.temp, tb, w.keys, w.skeys, w.vals, w.svals, R, end_bit, capturing(st), st);
         if (e != hipSuccess) return (int)e;
     }
     hipLaunchKernelGGL(emb_row_ranges_kernel, dim3((unsigned)((V + 1 + 255) / 256)), dim3(256), 0, st, w.skeys, R, V,

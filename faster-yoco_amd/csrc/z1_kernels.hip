@@ -539,6 +539,36 @@ __global__ __launch_bounds__(kBindPerLaunch) void set_grads_kernel(Row* rows, Gr
     r->vec = ga ? (kVecG | (r->pmv_aligned ? kVecAll : 0)) : 0;
 }
 
+// All pointers of up to kRebindPerLaunch rows (z1_table_rebind), passed by value like GradBind.
+constexpr int kRebindPerLaunch = 64;
+struct RowBind {
+    const void* g[kRebindPerLaunch];
+    float* p[kRebindPerLaunch];
+    float* m[kRebindPerLaunch];
+    float* v[kRebindPerLaunch];
+    uint16_t* p16[kRebindPerLaunch];
+    int32_t row[kRebindPerLaunch];
+    int32_t count;
+    int32_t g_align;
+};
+
+__global__ __launch_bounds__(kRebindPerLaunch) void rebind_rows_kernel(Row* rows, RowBind b) {
+    const int i = threadIdx.x;
+    if (i >= b.count) return;
+    Row* r = rows + b.row[i];
+    const uintptr_t pmv = reinterpret_cast<uintptr_t>(b.p[i]) | reinterpret_cast<uintptr_t>(b.m[i]) |
+                          reinterpret_cast<uintptr_t>(b.v[i]);
+    const bool pmv_ok = (pmv & 15) == 0 && (reinterpret_cast<uintptr_t>(b.p16[i]) & 7) == 0;
+    const bool ga = (reinterpret_cast<uintptr_t>(b.g[i]) & (uintptr_t)(b.g_align - 1)) == 0;
+    r->g = b.g[i];
+    r->p = b.p[i];
+    r->m = b.m[i];
+    r->v = b.v[i];
+    r->p16 = b.p16[i];
+    r->pmv_aligned = pmv_ok;
+    r->vec = ga ? (kVecG | (pmv_ok ? kVecAll : 0)) : 0;
+}
+
 // ------------------------------------------------------------------------------------- scale / cast passes
 __global__ __launch_bounds__(kThreads) void scale_up_kernel(const uint16_t* __restrict__ g16, float* __restrict__ g32,
                                                             const float* __restrict__ factor, int64_t n, int vec) {
@@ -676,6 +706,7 @@ struct z1_table {
     int32_t* chunk_row;
     std::vector<int64_t> first_chunk;   // host: first chunk of each row given to z1_table_create, + the total
     std::vector<int32_t> dev_row;       // host: device row of each row given to z1_table_create (-1: empty)
+    std::vector<int64_t> row_numel;     // host: elements of each row given to z1_table_create
     int nrows;            // rows given to z1_table_create, empty ones included
     int nrows_dev;        // non-empty rows (the device table)
     int g_dtype;
@@ -712,12 +743,14 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     h.reserve(nrows);
     std::vector<int64_t> first((size_t)nrows + 1);
     std::vector<int32_t> dev_row((size_t)nrows, -1);
+    std::vector<int64_t> row_numel((size_t)nrows, 0);
     int64_t chunks = 0, numel = 0;
     int has_pmv = 1;
     for (int i = 0; i < nrows; ++i) {
         const z1_tensor& t = rows[i];
         if (t.n < 0 || t.n > (int64_t)INT32_MAX * kChunk) return Z1_E_SIZE;   // also keeps the sums below in range
         first[i] = chunks;
+        row_numel[i] = t.n;
         if (t.n == 0) continue;
         if (!t.g) return Z1_E_NULL;
         Row r;
@@ -762,6 +795,7 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     tb->nchunks = chunks;
     tb->first_chunk.swap(first);
     tb->dev_row.swap(dev_row);
+    tb->row_numel.swap(row_numel);
     tb->rows = nullptr;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&tb->rows), img.size());
     if (e != hipSuccess) {
@@ -801,6 +835,45 @@ int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* 
     if (numel) *numel = table->numel;
     if (nchunks) *nchunks = table->nchunks;
     if (nrows) *nrows = table->nrows;             // the rows given to z1_table_create, empty ones included
+    return Z1_OK;
+}
+
+int z1_table_rebind(z1_table* table, const z1_tensor* rows, int nrows, void* stream) {
+    if (!table || (nrows > 0 && !rows)) return Z1_E_NULL;
+    if (nrows != table->nrows) return Z1_E_SIZE;
+    int dev = 0;
+    int rc = check_table_device(table, &dev);
+    if (rc) return rc;
+    for (int i = 0; i < nrows; ++i) {                  // the same sizes, and every pointer a launch will follow
+        if (rows[i].n != table->row_numel[i]) return Z1_E_SIZE;
+        if (table->dev_row[i] < 0) continue;           // an empty row
+        if (!rows[i].g) return Z1_E_NULL;
+        if (table->has_pmv && (!rows[i].p || !rows[i].m || !rows[i].v)) return Z1_E_NULL;
+    }
+    RowBind b;
+    memset(&b, 0, sizeof(b));
+    b.g_align = table->g_dtype == Z1_F32 ? 16 : 8;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    for (int i = 0; i < nrows; ++i) {
+        if (table->dev_row[i] < 0) continue;
+        const int k = b.count;
+        b.g[k] = rows[i].g;
+        b.p[k] = rows[i].p;
+        b.m[k] = rows[i].m;
+        b.v[k] = rows[i].v;
+        b.p16[k] = rows[i].p16;
+        b.row[k] = table->dev_row[i];
+        if (++b.count == kRebindPerLaunch) {
+            hipLaunchKernelGGL(rebind_rows_kernel, dim3(1), dim3(kRebindPerLaunch), 0, s, table->rows, b);
+            rc = launch_status();
+            if (rc) return rc;
+            b.count = 0;
+        }
+    }
+    if (b.count) {
+        hipLaunchKernelGGL(rebind_rows_kernel, dim3(1), dim3(kRebindPerLaunch), 0, s, table->rows, b);
+        return launch_status();
+    }
     return Z1_OK;
 }
 

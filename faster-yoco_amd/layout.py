@@ -20,16 +20,22 @@ def greedy_partition(numels, world):
     return owner, sizes
 
 
+def owner_slots(numels, owners, world):
+    """Given each parameter's owner: (offset of each parameter inside its owner's segment, model order; elements
+    per owner; seg = the largest owner total, the segment length of the flat buffer)."""
+    totals = [0] * world
+    local = []
+    for n, r in zip(numels, owners):
+        local.append(totals[r])
+        totals[r] += int(n)
+    return local, totals, (max(totals) if totals else 0)
+
+
 def segments(numels, world):
-    """Offsets of every parameter in the flat buffer (zero1_fast.py:66-74) and seg."""
-    owner, sizes = greedy_partition(numels, world)
-    seg = max(sizes) if sizes else 0
-    offs = [r * seg for r in range(world)]
-    where = []
-    for n, r in zip(numels, owner):
-        where.append(offs[r])
-        offs[r] += int(n)
-    return owner, where, seg
+    """Owners, offsets of every parameter in the flat buffer of world * seg elements (zero1_fast.py:66-74), seg."""
+    owner, _ = greedy_partition(numels, world)
+    local, _, seg = owner_slots(numels, owner, world)
+    return owner, [r * seg + o for r, o in zip(owner, local)], seg
 
 
 def place_params(params, world, device=None):

@@ -50,15 +50,12 @@ class FlatShard:
         self.v = torch.zeros(self.total, dtype=torch.float32, device=dev)
         self.g = torch.zeros(self.total, dtype=grad_dtype, device=dev)
         self.p16 = torch.zeros(self.total, dtype=torch.bfloat16, device=dev) if bf16_copy else None
-        self.table = ops.Table(self._rows(), dev)
+        # flat form: the operators take the five buffers, the table their rows' offsets
+        self.table = ops.Table.flat(self.offsets, self.numels, self.g, self.p, self.m, self.v, self.p16)
 
-    def _rows(self):
-        rows = []
-        for o, n in zip(self.offsets, self.numels):
-            sl = slice(o, o + n)
-            rows.append((self.g[sl], self.p[sl], self.m[sl], self.v[sl],
-                         None if self.p16 is None else self.p16[sl], n))
-        return rows
+    def buffers(self):
+        """The (g, p, m, v, p16) buffer lists the table's operators take."""
+        return self.table.bound
 
     def row_elements(self, row_begin, row_end):
         """[first, last) positions in the flat buffers spanned by the tensors row_begin .. row_end - 1."""

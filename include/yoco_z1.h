@@ -79,6 +79,13 @@ int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* 
  * element-wise path. */
 int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* stream);
 
+/* Points every row of the table at new tensors: rows as given to z1_table_create (the same count and the same n per
+ * row, else Z1_E_SIZE; p, m, v present wherever the table had them).  Enqueued on the stream like z1_table_set_grads
+ * (no allocation, no host synchronisation).  For callers whose tensors move as a whole -- a framework that runs the
+ * update on copies of the state, as torch's functionalization may -- so that one table made at set-up follows
+ * them. */
+int z1_table_rebind(z1_table* table, const z1_tensor* rows, int nrows, void* stream);
+
 /* Owner-side sum (replaces the Triton kernel _sum_slots, yoco/models/decoder/ce_reduce.py:59-74, launched by
  * CEReduce._sum :178-183):
  *   for e in [0,n): acc = 0f; for k = 0..world-1: acc += float(contrib[k][e]); out_avg[e] = bf16(acc * scale)
@@ -202,11 +209,12 @@ int z1_cast_bf16(const float* p32, uint16_t* p16, int64_t n, void* stream);
  * sum rounded to bf16 and added to the bf16 row.  Every row of
  * out is written (rows without occurrences, padding_idx and ids outside [0, V) give zeros).  workspace: device
  * memory of z1_embedding_backward_workspace(R, D, V) bytes (with D <= 2^24: about 4/7 of R x D x 4 bytes for
- * the fp32 run partials of frequent ids, and R x 16 + V x 4 bytes plus the radix sort's storage).  */
+ * the fp32 run partials of frequent ids, and R x 16 + V x 4 bytes plus the sort's storage).  */
 int z1_embedding_backward(const int64_t* ids, const uint16_t* grad, int64_t R, int64_t D, int64_t V,
                           int64_t padding_idx, float scale, int scale_mode, uint16_t* out, void* workspace,
                           int64_t workspace_bytes, void* stream);
 int64_t z1_embedding_backward_workspace(int64_t R, int64_t D, int64_t V);
+/* (z1_embedding_backward records no memset into a graph being captured: it sorts with a memset-free sort then.) */
 
 /* Text for a return code (negative: argument errors; positive: hipError_t). */
 const char* z1_strerror(int code);

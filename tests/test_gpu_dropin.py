@@ -144,6 +144,10 @@ def test_zero1_fast_trainer_sequence(pkg, dev, switches, reduce_owner):
         opt.step()
         torch.cuda.synchronize()
         assert opt._multiply_factor == 1.0
+        if not sw.get('FOLD_SCALE'):
+            # the masters' FP32 gradients are written as the reference writes them: fp32(float(g16) * factor)
+            for i, p32 in enumerate(opt.fp32_params):
+                assert np.array_equal(bits(p32.grad).ravel(), oracle.scale_up(grads16[i], fac_gpu).view(np.uint32)), i
         new = [oracle.adam_cast(g, *st_, step=step, factor=fac_gpu, **HP) for g, st_ in zip(grads16, state)]
         for i, p in enumerate(params):
             po, mo, vo, p16 = new[i]
@@ -155,6 +159,38 @@ def test_zero1_fast_trainer_sequence(pkg, dev, switches, reduce_owner):
         state = [(po, mo, vo) for po, mo, vo, _ in new]
         opt.zero_grad()
         assert all(p.grad is None for p in params)
+    zero1_fast.configure(ENABLED=False)
+
+
+def test_zero1_fast_default_fold_switch_writes_master_grads(pkg, dev):
+    """Under the default YOCO_Z1_FOLD_SCALE (unset: off) the step leaves the reference's observable state: every
+    owned master's .grad holds fp32(float(g16) * factor) (zero1_fast.py:175-192) after the step."""
+    from faster_yoco_amd import zero1_fast
+    default_fold = zero1_fast._switch('YOCO_Z1_FOLD_SCALE')
+    assert default_fold is False
+    zero1_fast.configure(ENABLED=True, FUSED_ADAM=True, ONE_PASS=True, SCALE_KERNEL=True, ALLGATHER=False,
+                         PARAM_VIEWS=False, REDUCE_OWNER=False, FOLD_SCALE=default_fold)
+
+    class Mixin(fakes.FakeMixin):
+        pass
+
+    zero1_fast._ORIG.clear()
+    assert zero1_fast.install(Mixin)
+
+    class Opt(Mixin, fakes.FakeFP16Optimizer):
+        pass
+
+    params = bf16_params(dev, 3)
+    opt = Opt(params, lr=HP['lr'], betas=(HP['beta1'], HP['beta2']), eps=HP['eps'], weight_decay=HP['weight_decay'])
+    set_grads(params, 31)
+    grads16 = [bits(p.grad).ravel().copy() for p in params]
+    opt.multiply_grads(8 / torch.tensor(16384.0, device=dev))
+    opt.clip_grad_norm(0.05)
+    fac = float(opt._multiply_factor.item())
+    opt.step()
+    torch.cuda.synchronize()
+    for i, p32 in enumerate(opt.fp32_params):
+        assert np.array_equal(bits(p32.grad).ravel(), oracle.scale_up(grads16[i], fac).view(np.uint32)), i
     zero1_fast.configure(ENABLED=False)
 
 
@@ -248,7 +284,7 @@ def test_zero1_fast_measured_switch_set_with_placed_params(pkg, dev):
             fac = float(opt._multiply_factor.item())
             opt.step()
             torch.cuda.synchronize()
-            assert opt._z1['placed']
+            assert opt._z1.placed
             for i, p in enumerate(params):
                 po, mo, vo, p16 = oracle.adam_cast(grads16[i], *state[i], step=step, factor=fac, **HP)
                 assert np.array_equal(bits(p).ravel(), p16), i            # the placed view itself was written

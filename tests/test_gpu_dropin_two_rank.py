@@ -93,7 +93,7 @@ def test_two_rank_clip_and_exchange(pkg, dev, monkeypatch):
             oss._param_to_rank = {p32: o for p32, o in zip(opt.fp32_params, owner)}
             oss.rank, oss.world_size, oss.group, oss._local_to_global_rank = r, 2, 'group', [0, 1]
             opt.fp32_optimizer = FakeFairseqOptimizer(oss)
-            assert zero1_fast._setup(opt)['placed']                       # this rank's placement is captured
+            assert zero1_fast._plan(opt).placed                            # this rank's placement is captured
             for p, g, o in zip(params, grads16, owner):                   # the owner holds the reduced grads
                 p.grad = (torch.from_numpy(g.view(np.int16)).to(dev).view(torch.bfloat16).view(p.shape)
                           if o == r else None)

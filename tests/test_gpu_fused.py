@@ -148,7 +148,7 @@ def test_set_grads_matches_a_new_table(pkg, dev):
     for X, Y in ((ps, P2), (ms, M2), (vs, V2)):
         for a, b in zip(X, Y):
             assert np.array_equal(f32_bits(a), f32_bits(b))
-    with pytest.raises(RuntimeError, match='rows'):
+    with pytest.raises(RuntimeError, match='one tensor per table row'):
         ta.set_grads(g2[:-1])
 
 
@@ -165,9 +165,10 @@ def test_table_cache_rebinds_instead_of_rebuilding(pkg, dev):
     for step in range(1, 6):
         gs = [torch.randn(n, device=dev) * 1e-3 for n in sizes]
         keep.append(gs)                                    # distinct addresses every step
-        table = cache.get([(g, a, b, c, None, g.numel()) for g, a, b, c in zip(gs, p, m, v)], dev)
+        rows = [(g, a, b, c, None, g.numel()) for g, a, b, c in zip(gs, p, m, v)]
+        table = cache.get(rows, dev)
         bc1, bc2 = ops.bias_corrections(0.9, 0.95, step)
-        ops.adam_cast(table, None, 3e-4, 0.9, 0.95, 1e-8, bc1, bc2, 0.1, 1)
+        ops.adam_cast(table, None, 3e-4, 0.9, 0.95, 1e-8, bc1, bc2, 0.1, 1, tensors=ops.rows_lists(rows))
         torch.cuda.synchronize()
         for i, g in enumerate(gs):
             po, mo, vo, _ = oracle.adam_cast(g.cpu().numpy(), *[x.copy() for x in state[i]], lr=3e-4, beta1=0.9,

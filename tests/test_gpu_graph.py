@@ -150,3 +150,42 @@ def test_device_bias_corrections_equal_host_rounding(pkg, dev):
     bc = torch.zeros(2, dtype=torch.float32, device=dev)
     ops.bias_corrections_step(step, 0.9, 0.95, bc, bias_correction=0)
     assert bc.tolist() == [1.0, 1.0]
+
+
+@pytest.mark.parametrize('R,zipf', [(16384, False), (16384, True), (2048, False)])
+def test_owner_embedding_grad_graph_replays_match_eager(pkg, dev, R, zipf):
+    """The owner's embedding gradient (OwnerEmbeddingGrad: output and workspace made once) captured in a HIP graph
+    and replayed on new ids and rows copied into its static inputs, three times with eager work in between: every
+    replay bit-identical to the eager call on the same inputs, and to torch's aten + x 1/8 (the reference's
+    layer_graphs.py:92-93).  The sort it runs clears nothing with memsets."""
+    from faster_yoco_amd import embedding
+    D, V = 3072, 100288
+    gen = torch.Generator(device='cpu').manual_seed(R + zipf)
+
+    def inputs():
+        if zipf:
+            z = np.random.default_rng(int(torch.randint(0, 1 << 30, (1,), generator=gen))).zipf(1.2, R) - 1
+            ids = torch.from_numpy(np.where(z < V, z, 0).astype(np.int64))
+        else:
+            ids = torch.randint(0, V, (R,), generator=gen)
+        return (torch.randn(R, D, generator=gen) * 1e-2).to(torch.bfloat16).to(dev), ids.to(dev)
+
+    plan = embedding.OwnerEmbeddingGrad(R, D, V, -1, 8, dev)
+    g_static, i_static = inputs()
+    plan(g_static, i_static)                            # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan(g_static, i_static)
+    for _ in range(3):
+        g_new, i_new = inputs()
+        g_static.copy_(g_new)
+        i_static.copy_(i_new)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = plan.out.clone()
+        eager = embedding.owner_embedding_grad(g_new, i_new, V, -1, 8)      # eager work between the replays
+        aten = torch.ops.aten.embedding_dense_backward(g_new, i_new, V, -1, False).mul_(1.0 / 8)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), eager.view(torch.int16))
+        assert torch.equal(got.view(torch.int16), aten.view(torch.int16))
