@@ -39,10 +39,15 @@ def algorithmic_bytes(cfg, n):
     return 34 * n, 30 * n, 30            # norm (4) + Adam with fp32 g (16 in, 12 out, 2 bf16 out)
 
 
+def traffic_file(kernel, workload):
+    return os.path.join('profiles', f'{kernel}_{workload}_traffic.json')
+
+
 def load_traffic(kernel, workload):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), from a
-    committed summary under profiles/, or None."""
-    path = os.path.join(ROOT, 'profiles', f'{kernel}_{workload}_traffic.json')
+    """HBM bytes per launch measured by rocprofv3 --pmc (read / write request counts by size, which agree with the
+    copy-calibrated FETCH_SIZE + WRITE_SIZE), from the committed summary under profiles/, or None.  Not measured in
+    this run: counters need their own profiler runs."""
+    path = os.path.join(ROOT, traffic_file(kernel, workload))
     if not os.path.exists(path):
         return None
     with open(path) as f:
@@ -285,6 +290,8 @@ def main():
     ap.add_argument('--dropin', action='store_true',
                     help='also time FusedAdamCast over the 38 C2 tensors allocated one by one (its launches share '
                          'the Adam kernel with the timed steps, so a kernel trace of the default run stays clean)')
+    ap.add_argument('--no-side', action='store_true',
+                    help='skip the side measurements (trainer scalar chain, embedding gradient), e.g. for counter runs')
     ap.add_argument('--calibrate-copy', action='store_true',
                     help='only run 5 plain 1 GiB device copies (the reference traffic for rocprofv3 counters)')
     args = ap.parse_args()
@@ -390,11 +397,14 @@ def main():
         'roofline': {'bound': 'hbm', 'kernel': 'adam_cast_kernel', 'achieved': round(achieved, 1),
                      'peak': PEAK_HBM_GBPS, 'unit': 'GB/s', 'frac': round(achieved / PEAK_HBM_GBPS, 4),
                      'traffic': load_traffic('adam_cast', cfg),
+                     'traffic_source': (traffic_file('adam_cast', cfg) + ' (rocprofv3 --pmc, committed; not measured '
+                                        'in this run)') if load_traffic('adam_cast', cfg) else None,
                      'bytes_per_param': adam_bpp, 'params_per_launch': n},
         'cpu_baseline': cpu,
-        'trainer_scalar_chain_us': glue_timing(opt, hp),
-        'owner_embedding_grad_ms': embedding_timing(dev),
     }
+    if not args.no_side:
+        out['trainer_scalar_chain_us'] = glue_timing(opt, hp)
+        out['owner_embedding_grad_ms'] = embedding_timing(dev)
     if args.dropin:
         out['dropin_multi_tensor_adam'] = dropin_timing(dev, hp, step0)
     if args.pipeline > 0:
