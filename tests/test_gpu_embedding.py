@@ -126,3 +126,19 @@ def test_matches_oracle_and_edge_cases(pkg, dev):
     assert not out.float().abs().sum().item()
     with pytest.raises(RuntimeError, match='scale_grad_by_freq'):
         embedding.embedding_dense_backward(gt, torch.from_numpy(ids).to(dev), V, -1, True)
+
+
+def test_aten_few_indices_order_known_answer(pkg, dev):
+    """Guard of the bit-exact claim for at most 3072 rows, whose order follows torch's own ROCm aten kernel (chunks
+    of 16 indices, each chunk's fp32 sum rounded to bf16 before it is added to the row).  On one id, rows 1.0, 2^-9,
+    fourteen zeros, 2^-8: chunks of 16 give 0x3F80; one chunk of 32, or the sort path, 0x3F81.  If a torch build
+    walks the indices otherwise, this fails here, loudly, instead of the bf16 copies drifting in their last bit."""
+    from faster_yoco_amd import embedding
+    vals = [1.0, 2.0 ** -9] + [0.0] * 14 + [2.0 ** -8]
+    g = torch.tensor(vals, dtype=torch.float32).reshape(-1, 1).to(torch.bfloat16).to(dev)
+    ids = torch.zeros(len(vals), dtype=torch.int64, device=dev)
+    aten = torch.ops.aten.embedding_dense_backward(g, ids, 1, -1, False)
+    ours = embedding.embedding_dense_backward(g, ids, 1, -1)
+    torch.cuda.synchronize()
+    assert int(aten.view(torch.int16).item()) & 0xFFFF == 0x3F80, 'torch\'s few-indices order changed'
+    assert int(ours.view(torch.int16).item()) & 0xFFFF == 0x3F80
