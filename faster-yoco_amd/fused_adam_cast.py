@@ -6,11 +6,16 @@ an fp32 master -> the BF16 tensor to write), called by fairseq's FusedAdamV2.ste
 arguments, and collects in ``.cast`` the addresses of the masters whose BF16 copy it wrote.  Internally:
   * all the call's tensors go to one ``torch.ops.yoco_z1.adam_cast_`` launch over a table (cached by the rows'
     sizes, bound to the call's tensors), where the reference launches one Triton kernel per tensor;
+  * what a parameter list needs -- its table, the BF16 destinations found in ``dest``, the masters they belong to
+    -- is worked out once per list of masters (keyed by their addresses and sizes, as ``dest`` is keyed by
+    address) and reused while the list recurs; each call's tensors are still checked, by the operator;
   * ``fold`` / ``fold_factor`` (set by zero1_fast.step under YOCO_Z1_FOLD_SCALE=1) name masters whose BF16 gradient
     the kernel reads times the factor, in place of the FP32 gradient a scale pass would have written: the same
     products g' = fp32(float(g16) * factor), 6 bytes per element less traffic.
 ``scale_up`` keeps ``fused_adam_cast.py:84-89``'s signature.
 """
+from collections import OrderedDict
+
 import torch
 
 from . import ops
@@ -28,26 +33,32 @@ class FusedAdamCast:
         self.fold = {}                    # master address -> BF16 gradient read in place of the FP32 one
         self.fold_factor = None           # the 1-element fp32 device factor of the folded gradients
         self._tables = ops.TableCache()
+        self._plans = OrderedDict()       # masters' (address, size)s -> (table, BF16 destinations, addresses)
 
     def __call__(self, chunk_size, noop_flag, tensor_lists, lr, beta1, beta2, eps, step, mode, bias_correction,
                  weight_decay):
         if int(mode) not in (0, 1):
             raise RuntimeError(f'fused_adam_cast: unsupported adam mode {mode}')
         bc1, bc2 = ops.bias_corrections(beta1, beta2, step, bias_correction)
+        if not self.fold:
+            g, p, m, v = tensor_lists
+            if not p:
+                return
+            key = tuple([(t.data_ptr(), t.numel()) for t in p])
+            plan = self._plans.get(key)
+            if plan is None:
+                plan = self._plan(key, tensor_lists)
+            table, p16, written = plan
+            ops.adam_cast(table, None, lr, beta1, beta2, eps, bc1, bc2, weight_decay, int(mode),
+                          tensors=(g, p, m, v, p16))
+            self.cast.update(written)
+            return
         groups = {False: [], True: []}    # rows reading the FP32 gradient / a folded BF16 one
         written = []
         for g, p, m, v in zip(*tensor_lists):
-            if not (g.dtype == p.dtype == m.dtype == v.dtype == torch.float32 and g.is_contiguous()
-                    and p.is_contiguous() and m.is_contiguous() and v.is_contiguous()):
-                raise RuntimeError('fused_adam_cast: expected contiguous fp32 tensors')
-            n = p.numel()
-            if g.numel() != n or m.numel() != n or v.numel() != n:
-                raise RuntimeError('fused_adam_cast: tensor sizes differ within a row')
+            n, d = self._row(g, p, m, v)
             key = p.data_ptr()
-            d = self.dest.get(key)
             if d is not None:
-                if d.dtype != torch.bfloat16 or not d.is_contiguous() or d.numel() != n:
-                    raise RuntimeError('fused_adam_cast: the bf16 destination must be a contiguous bf16 view')
                 written.append(key)
             g16 = self.fold.get(key)
             if g16 is not None and (g16.dtype != torch.bfloat16 or not g16.is_contiguous() or g16.numel() != n):
@@ -61,6 +72,34 @@ class FusedAdamCast:
                 ops.adam_cast(table, self.fold_factor if folded else None, lr, beta1, beta2, eps, bc1, bc2,
                               weight_decay, int(mode), tensors=ops.rows_lists(rows))
         self.cast.update(written)
+
+    def _row(self, g, p, m, v):
+        """Checked size and BF16 destination (or None) of one row."""
+        if not (g.dtype == p.dtype == m.dtype == v.dtype == torch.float32 and g.is_contiguous()
+                and p.is_contiguous() and m.is_contiguous() and v.is_contiguous()):
+            raise RuntimeError('fused_adam_cast: expected contiguous fp32 tensors')
+        n = p.numel()
+        if g.numel() != n or m.numel() != n or v.numel() != n:
+            raise RuntimeError('fused_adam_cast: tensor sizes differ within a row')
+        d = self.dest.get(p.data_ptr())
+        if d is not None and (d.dtype != torch.bfloat16 or not d.is_contiguous() or d.numel() != n):
+            raise RuntimeError('fused_adam_cast: the bf16 destination must be a contiguous bf16 view')
+        return n, d
+
+    def _plan(self, key, tensor_lists):
+        """Table, BF16 destination list and written addresses for a list of masters (checked row by row)."""
+        rows, written = [], []
+        for g, p, m, v in zip(*tensor_lists):
+            n, d = self._row(g, p, m, v)
+            if d is not None:
+                written.append(p.data_ptr())
+            rows.append((g, p, m, v, d, n))
+        table = self._tables.get(rows, rows[0][1].device)
+        plan = (table, ops.rows_lists(rows)[4], tuple(written))
+        self._plans[key] = plan
+        while len(self._plans) > 8:
+            self._plans.popitem(last=False)
+        return plan
 
 
 def scale_up(g16, g32, factor):

@@ -83,6 +83,15 @@ def test_fused_adam_cast_errors(pkg, dev):
     fa = FusedAdamCast({x.data_ptr(): torch.zeros(64, device=dev)})
     with pytest.raises(RuntimeError, match='bf16 destination'):
         fa(0, None, [[x], [x], [x.clone()], [x.clone()]], 1e-3, 0.9, 0.95, 1e-8, 1, 1, 1, 0.0)
+    # a list of masters seen before reuses its plan; the operator still checks every tensor of the call
+    fa = FusedAdamCast({})
+    m, v = x.clone(), x.clone()
+    fa(0, None, [[x.clone()], [x], [m], [v]], 1e-3, 0.9, 0.95, 1e-8, 1, 1, 1, 0.0)
+    with pytest.raises(RuntimeError, match='expected contiguous fp32 tensors'):
+        fa(0, None, [[x.t()], [x], [m], [v]], 1e-3, 0.9, 0.95, 1e-8, 2, 1, 1, 0.0)
+    with pytest.raises(RuntimeError, match='row 0 has 32 elements, the table 64'):
+        fa(0, None, [[x.clone()], [x], [m[:4]], [v]], 1e-3, 0.9, 0.95, 1e-8, 2, 1, 1, 0.0)
+    fa(0, None, [[], [], [], []], 1e-3, 0.9, 0.95, 1e-8, 2, 1, 1, 0.0)          # empty lists: nothing to do
 
 
 # ---------------------------------------------------------------------------------------------- zero1_fast

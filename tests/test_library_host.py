@@ -113,6 +113,29 @@ def test_operators_refuse_cpu_tensors(pkg):
                                      -1, 1.0, 0, torch.zeros(64, dtype=torch.uint8))
 
 
+def test_operator_library_host_entry_points(pkg):
+    """libyoco_z1_torch.so is bound to the C ABI library and registers tables with checked arguments (no device
+    work: a registered handle is only recorded)."""
+    import ctypes
+    from faster_yoco_amd import _lib, library
+    L = library.OPS_LIB
+    assert L.z1t_init(_lib.lib()._name.encode()) == 0
+    assert L.z1t_init(b'/nonexistent/libyoco_z1.so') == -1            # not a loaded library: refused
+    assert L.z1t_init(_lib.lib()._name.encode()) == 0                  # bound again to the right one
+    rows = (_lib.Z1Tensor * 2)(_lib.Z1Tensor(None, None, None, None, None, 10),
+                               _lib.Z1Tensor(None, None, None, None, None, 6))
+    fake = ctypes.c_void_p(0x1000)
+    assert L.z1t_table_register(None, 0, 0, 0, 2, rows, None) == -1   # no table
+    assert L.z1t_table_register(fake, 0, 7, 0, 2, rows, None) == -1   # unknown gradient dtype
+    assert L.z1t_table_register(fake, 0, 0, 0, -1, rows, None) == -1  # negative row count
+    bad = (ctypes.c_int64 * 2)(0, -4)
+    assert L.z1t_table_register(fake, 0, 0, 0, 2, rows, bad) == -1    # negative flat offset
+    offs = (ctypes.c_int64 * 2)(0, 16)
+    assert L.z1t_table_register(fake, 0, 0, 0, 2, rows, offs) == 0
+    L.z1t_table_forget(fake)
+    L.z1t_table_forget(fake)                                           # forgetting twice is harmless
+
+
 def _run(script, env_extra, prelude=''):
     env = dict(os.environ)
     for k in list(env):
