@@ -154,7 +154,8 @@ def dropin_timing(dev, hp, step, reps=10):
     """The drop-in surface at C2's size: FusedAdamCast called with amp_C.multi_tensor_adam's signature (as
     fairseq's FusedAdamV2.step calls it) over the 38 C2 tensors allocated one by one (the reference's
     per-parameter layout, BF16 destinations as views of one flat buffer), once with fp32 gradients and once with
-    the BF16 gradients folded in (zero1_fast's default); HIP events on the current stream, ms per call."""
+    the BF16 gradients folded in (YOCO_Z1_FOLD_SCALE=1); HIP events on the current stream, ms per call, and the
+    host's time per call (wall clock of the enqueues, which the GPU's 2 ms per call keeps from ever waiting)."""
     import torch
     from faster_yoco_amd import configs
     from faster_yoco_amd.fused_adam_cast import FusedAdamCast
@@ -185,11 +186,14 @@ def dropin_timing(dev, hp, step, reps=10):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record()
+        t0 = time.perf_counter()
         for _ in range(reps):
             call()
+        host = time.perf_counter() - t0
         e1.record()
         torch.cuda.synchronize()
         out[name] = round(e0.elapsed_time(e1) / reps, 4)
+        out[name.replace('_ms', '_host_us')] = round(host / reps * 1e6, 1)
         fa.cast.clear()
     fa.fold, fa.fold_factor = {}, None
     return out

@@ -4,9 +4,9 @@ The directory name is not a Python identifier; the package is imported as ``fast
 root's ``faster_yoco_amd.py`` registers it under that name when the root is on sys.path).
 
 Modules
-    library          the path's kernels as PyTorch custom operators (torch.ops.yoco_z1.*) over the C ABI
+    library          loads the path's PyTorch operators (torch.ops.yoco_z1.*, C++ over the C ABI) + fake kernels
     ops              the public operations on tensors and tables (each a torch.ops.yoco_z1 call)
-    kernels          the ctypes launches behind the operators, and the tensor-offset tables
+    kernels          the tensor-offset tables (made through the C ABI, registered with the operators), helpers
     shard            flat HBM shard + FP16Optimizer-style optimizer (multiply_grads / clip_grad_norm / step)
     fused_adam_cast  drop-in for yoco/tasks/fused_adam_cast.py (FusedAdamCast, scale_up)
     zero1_fast       drop-in for yoco/tasks/zero1_fast.py (clip_grad_norm / step / zero_grad patches, layout)

@@ -1,5 +1,5 @@
-"""The public operations of the path, each a call of a ``torch.ops.yoco_z1`` custom operator (``library.py``) over
-the C ABI.  Every call enqueues on torch's current stream of the tensors' device, performs no host synchronisation
+"""The public operations of the path, each a call of a ``torch.ops.yoco_z1`` operator (C++ over the C ABI, loaded by
+``library.py``).  Every call enqueues on torch's current stream of the tensors' device, performs no host synchronisation
 and allocates nothing (tables are made once, at set-up; a Python-number factor and a device output may be mixed as
 the reference's fairseq surface mixes them).
 
