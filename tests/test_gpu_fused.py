@@ -176,3 +176,41 @@ def test_table_cache_rebinds_instead_of_rebuilding(pkg, dev):
             assert np.array_equal(f32_bits(p[i]), po.view(np.uint32))
             state[i] = (po, mo, vo)
     assert cache.builds == 1
+
+
+def test_operators_follow_moved_state_tensors(pkg, dev):
+    """The operator layer rebinds a table to whichever tensors a call passes: an update on copies of p, m, v (and a
+    new gradient, and no BF16 copies) equals the same update on a table made on those copies; the original state is
+    left untouched; a call naming an unknown table or tensors of the wrong size raises before any launch."""
+    from faster_yoco_amd import ops
+    Y = torch.ops.yoco_z1
+    sizes = [5000, 0, 1 << 14, 33]
+    gen = torch.Generator(device='cpu').manual_seed(9)
+    mk = lambda s: [(torch.randn(n, generator=gen) * s).to(dev) for n in sizes]
+    g, p, m, v = mk(1e-3), mk(0.02), mk(1e-4), [t.abs() for t in mk(1e-8)]
+    p16 = [torch.zeros(n, dtype=torch.bfloat16, device=dev) for n in sizes]
+    table = ops.Table([r + (r[0].numel(),) for r in zip(g, p, m, v, p16)], dev)
+    keep = [[t.clone() for t in X] for X in (p, m, v, p16)]
+    g2 = [t * 2 for t in g]
+    P, M, V = ([t.clone() for t in X] for X in (p, m, v))
+    args = (None, 3e-4, 0.9, 0.95, 1e-8, 0.5, 0.75, 0.1, 1, 0, len(sizes))
+    Y.adam_cast_(table.handle_int, g2, P, M, V, [], *args)           # moved: every stream, BF16 copies off
+    P2, M2, V2 = ([t.clone() for t in X] for X in (p, m, v))
+    fresh = ops.Table([(a, b, c, d, None, a.numel()) for a, b, c, d in zip(g2, P2, M2, V2)], dev)
+    Y.adam_cast_(fresh.handle_int, g2, P2, M2, V2, [], *args)
+    torch.cuda.synchronize()
+    for X, Z in ((P, P2), (M, M2), (V, V2)):
+        for a, b in zip(X, Z):
+            assert np.array_equal(f32_bits(a), f32_bits(b))
+    for X, K in zip((p, m, v, p16), keep):                            # the tensors the table was made on
+        for a, b in zip(X, K):
+            assert torch.equal(a, b)
+    Y.adam_cast_(table.handle_int, g, p, m, v, p16, *args)            # and back to them
+    torch.cuda.synchronize()
+    assert not torch.equal(p[0], keep[0][0]) and p16[0].abs().sum() > 0
+    with pytest.raises(RuntimeError, match='no live table'):
+        Y.adam_cast_(12345, g, p, m, v, p16, *args)
+    with pytest.raises(RuntimeError, match='row 0 has 4999 elements, the table 5000'):
+        Y.adam_cast_(table.handle_int, [g[0][1:]] + g[1:], p, m, v, p16, *args)
+    with pytest.raises(RuntimeError, match='rows \\[0, 9\\) outside'):
+        Y.adam_cast_(table.handle_int, g, p, m, v, p16, *args[:-1], 9)
