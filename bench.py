@@ -363,6 +363,7 @@ def main():
     t0 = time.perf_counter()
     for i in range(args.steps):
         one_step(events[i // every] if i % every == 0 else None)
+    enqueued = time.perf_counter() - t0                 # the host's share: every launch of the K steps enqueued
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
 
@@ -392,6 +393,7 @@ def main():
                    'eps': hp['eps'], 'weight_decay': hp['weight_decay'], 'max_norm': hp['max_norm'],
                    'algorithmic_bytes_per_step': step_bytes},
         'median_step_ms_events': round(step_ms[len(step_ms) // 2], 4),
+        'host_us_per_step': round(enqueued * 1e6 / args.steps, 1),
         'event_sampled_steps': len(events),
         'achieved_GBps': round(step_bytes / (ms_step * 1e-3) / 1e9, 1),
         'frac_of_peak': round(step_bytes / (ms_step * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
