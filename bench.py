@@ -153,12 +153,14 @@ def glue_timing(opt, hp, iters=200):
 def dropin_timing(dev, hp, step, reps=10):
     """The drop-in surface at C2's size: FusedAdamCast called with amp_C.multi_tensor_adam's signature (as
     fairseq's FusedAdamV2.step calls it) over the 38 C2 tensors allocated one by one (the reference's
-    per-parameter layout, BF16 destinations as views of one flat buffer), once with fp32 gradients and once with
-    the BF16 gradients folded in (YOCO_Z1_FOLD_SCALE=1); HIP events on the current stream, ms per call, and the
-    host's time per call (wall clock of the enqueues, which the GPU's 2 ms per call keeps from ever waiting)."""
+    per-parameter layout, BF16 destinations as views of one flat buffer): with fp32 gradients; after the
+    reference's scale pass (one scale_up per tensor writing the fp32 gradients, then Adam reading them); with the
+    BF16 gradients folded in and the fp32 gradients written by the same launch (zero1_fast's default); folded
+    without writing them (YOCO_Z1_FOLD_SCALE=1).  HIP events on the current stream, ms per call, and the host's
+    time per call (wall clock of the enqueues, which the GPU's 2 ms per call keeps from ever waiting)."""
     import torch
     from faster_yoco_amd import configs
-    from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+    from faster_yoco_amd.fused_adam_cast import FusedAdamCast, scale_up
     shapes = configs.shapes('c2')
     numels = [math.prod(s) for s in shapes]
     flat16 = torch.empty(sum(numels), dtype=torch.bfloat16, device=dev)
@@ -176,11 +178,20 @@ def dropin_timing(dev, hp, step, reps=10):
     noop = torch.zeros(1, dtype=torch.int32, device=dev)
     factor = torch.full((1,), 0.5, dtype=torch.float32, device=dev)
     out = {'tensors': len(shapes), 'params': sum(numels)}
-    for name, fold in (('fp32_grads_ms', False), ('folded_bf16_grads_ms', True)):
+    adam = lambda: fa(2048 * 32, noop, [gs, ps, ms, vs], hp['lr'], hp['betas'][0], hp['betas'][1], hp['eps'], step,
+                      1, 1, hp['weight_decay'])
+
+    def scale_then_adam():
+        for g16, g in zip(g16s, gs):
+            scale_up(g16, g, factor)
+        adam()
+    for name, fold, writes in (('fp32_grads_ms', False, False), ('scale_pass_then_adam_ms', None, False),
+                               ('folded_bf16_grads_written_ms', True, True), ('folded_bf16_grads_ms', True, False)):
+        fa.fold, fa.fold_factor, fa.fold_writes = {}, None, False
         if fold:
             fa.fold, fa.fold_factor = {p.data_ptr(): g for p, g in zip(ps, g16s)}, factor
-        call = lambda: fa(2048 * 32, noop, [gs, ps, ms, vs], hp['lr'], hp['betas'][0], hp['betas'][1], hp['eps'],
-                          step, 1, 1, hp['weight_decay'])
+            fa.fold_writes = writes
+        call = scale_then_adam if fold is None else adam
         for _ in range(3):
             call()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -195,7 +206,7 @@ def dropin_timing(dev, hp, step, reps=10):
         out[name] = round(e0.elapsed_time(e1) / reps, 4)
         out[name.replace('_ms', '_host_us')] = round(host / reps * 1e6, 1)
         fa.cast.clear()
-    fa.fold, fa.fold_factor = {}, None
+    fa.fold, fa.fold_factor, fa.fold_writes = {}, None, False
     return out
 
 

@@ -49,6 +49,7 @@ SIGNATURES = {
     'z1_owner_sum_update_noalloc': ([_P, _I, _I64, _F, _P, _P, ctypes.POINTER(Z1UpdateScalars), _P], _I),
     'z1_table_set_grads': ([_P, _P, _I, _P], _I),
     'z1_table_rebind': ([_P, ctypes.POINTER(Z1Tensor), _I, _P], _I),
+    'z1_table_set_grad_out': ([_P, _P, _I, _P], _I),
     'z1_grad_sumsq': ([_P, _P, _P], _I),
     'z1_grad_norm_clip': ([_P, _P, _P, _F, _P, _P, _P, _F, _P], _I),
     'z1_grad_update_scalars': ([_P, _P, ctypes.POINTER(Z1UpdateScalars), _P], _I),

@@ -185,12 +185,16 @@ __device__ __forceinline__ float load_g1(const void* g, int64_t i) {
     return bf16_to_f32(static_cast<const uint16_t*>(g)[i]);
 }
 
-template <int GDT, int MODE>
+// GOUT: the table carries FP32 gradient outputs (z1_table_set_grad_out): each row's g' = fp32(g * factor), the value
+// the update consumes, is also stored to gout[row] (NULL: not for that row) -- the FP32 gradient the reference's
+// scale pass writes before its Adam reads it back (yoco/tasks/zero1_fast.py:175-192, fused_adam_cast.py:75-89).
+template <int GDT, int MODE, bool GOUT>
 __global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row* __restrict__ rows,
                                                                        const int32_t* __restrict__ chunk_row,
                                                                        int64_t chunk_begin, int64_t chunk_end,
                                                                        const float* __restrict__ factor,
-                                                                       const float* __restrict__ bc, AdamK k) {
+                                                                       const float* __restrict__ bc, AdamK k,
+                                                                       float* const* __restrict__ gout) {
     const int lane = threadIdx.x & (kWave - 1);
     // chunks [chunk_begin, chunk_end), last chunk first: the end of the gradient is what the norm pass read last
     // (still in the MALL)
@@ -202,10 +206,12 @@ __global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row
         k.bc1 = bc[0];
         k.bc2 = bc[1];
     }
-    const Row r = rows[chunk_row[c]];
+    const int32_t ri = chunk_row[c];
+    const Row r = rows[ri];
+    float* const go = GOUT ? gout[ri] : nullptr;
     const int64_t base = (c - r.chunk0) * kChunk;
     const int64_t rem = r.n - base;
-    if (rem >= kChunk && (r.vec & kVecAll)) {
+    if (rem >= kChunk && (r.vec & kVecAll) && (!GOUT || (reinterpret_cast<uintptr_t>(go) & 15) == 0)) {
         f4 g[kGroups], p[kGroups], m[kGroups], v[kGroups];
 #pragma unroll
         for (int u = 0; u < kGroups; ++u) {
@@ -220,7 +226,8 @@ __global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row
 #pragma unroll
             for (int j = 0; j < kVec; ++j) {
                 float pj = p[u][j], mj = m[u][j], vj = v[u][j];
-                adam_elem<MODE>(g[u][j] * f, pj, mj, vj, k);
+                g[u][j] = g[u][j] * f;
+                adam_elem<MODE>(g[u][j], pj, mj, vj, k);
                 p[u][j] = pj;
                 m[u][j] = mj;
                 v[u][j] = vj;
@@ -236,12 +243,15 @@ __global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row
                 const u2 h = u2{pack_bf16(p[u][0], p[u][1]), pack_bf16(p[u][2], p[u][3])};
                 st(reinterpret_cast<u2*>(r.p16 + i), h);
             }
+            if (GOUT && go) st(reinterpret_cast<f4*>(go + i), g[u]);
         }
     } else {
         const int64_t cnt = rem < kChunk ? rem : kChunk;
         for (int64_t i = base + lane; i < base + cnt; i += kWave) {
             float pj = r.p[i], mj = r.m[i], vj = r.v[i];
-            adam_elem<MODE>(load_g1<GDT>(r.g, i) * f, pj, mj, vj, k);
+            const float gj = load_g1<GDT>(r.g, i) * f;
+            if (GOUT && go) go[i] = gj;
+            adam_elem<MODE>(gj, pj, mj, vj, k);
             r.p[i] = pj;
             r.m[i] = mj;
             r.v[i] = vj;
@@ -539,6 +549,13 @@ __global__ __launch_bounds__(kBindPerLaunch) void set_grads_kernel(Row* rows, Gr
     r->vec = ga ? (kVecG | (r->pmv_aligned ? kVecAll : 0)) : 0;
 }
 
+// FP32 gradient outputs of up to kBindPerLaunch rows (z1_table_set_grad_out), passed by value like the gradients.
+__global__ __launch_bounds__(kBindPerLaunch) void set_grad_out_kernel(float** gout, GradBind b) {
+    const int i = threadIdx.x;
+    if (i >= b.count) return;
+    gout[b.row[i]] = static_cast<float*>(const_cast<void*>(b.g[i]));
+}
+
 // All pointers of up to kRebindPerLaunch rows (z1_table_rebind), passed by value like GradBind.
 constexpr int kRebindPerLaunch = 64;
 struct RowBind {
@@ -712,6 +729,8 @@ struct z1_table {
     int g_dtype;
     int device;
     int has_pmv;          // every row has p, m and v
+    int gout_rows;        // rows with an FP32 gradient output (z1_table_set_grad_out), as last enqueued
+    float** gout;         // device, in the same allocation: the output of each device row (NULL: none)
     int64_t numel;
     int64_t nchunks;
 };
@@ -775,9 +794,10 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     int dev = 0;
     int rc = current_device(&dev);
     if (rc) return rc;
-    // host image of [rows][chunk -> row], copied in one transfer
+    // host image of [rows][chunk -> row][gradient outputs, all NULL], copied in one transfer
     const size_t rows_bytes = sizeof(Row) * h.size();
-    std::vector<unsigned char> img(rows_bytes + sizeof(int32_t) * (size_t)chunks + 64, 0);
+    const size_t gout_off = (rows_bytes + sizeof(int32_t) * (size_t)chunks + 15) & ~(size_t)15;
+    std::vector<unsigned char> img(gout_off + sizeof(float*) * h.size() + 64, 0);
     if (rows_bytes) memcpy(img.data(), h.data(), rows_bytes);
     int32_t* map = reinterpret_cast<int32_t*>(img.data() + rows_bytes);
     for (size_t i = 0; i < h.size(); ++i) {
@@ -803,6 +823,8 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
         return (int)e;
     }
     tb->chunk_row = reinterpret_cast<int32_t*>(reinterpret_cast<unsigned char*>(tb->rows) + rows_bytes);
+    tb->gout = reinterpret_cast<float**>(reinterpret_cast<unsigned char*>(tb->rows) + gout_off);
+    tb->gout_rows = 0;
     e = hipMemcpy(tb->rows, img.data(), img.size(), hipMemcpyHostToDevice);
     if (e != hipSuccess) {
         (void)hipFree(tb->rows);
@@ -906,6 +928,39 @@ int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* s
         hipLaunchKernelGGL(set_grads_kernel, dim3(1), dim3(kBindPerLaunch), 0, s, table->rows, b);
         return launch_status();
     }
+    return Z1_OK;
+}
+
+int z1_table_set_grad_out(z1_table* table, float* const* g32, int nrows, void* stream) {
+    if (!table) return Z1_E_NULL;
+    if (g32 && nrows != table->nrows) return Z1_E_SIZE;
+    int dev = 0;
+    int rc = check_table_device(table, &dev);
+    if (rc) return rc;
+    GradBind b;
+    b.count = 0;
+    b.g_align = 16;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    int set = 0;
+    for (int i = 0; i < table->nrows; ++i) {
+        if (table->dev_row[i] < 0) continue;
+        float* o = g32 ? g32[i] : nullptr;
+        set += o != nullptr;
+        b.g[b.count] = o;
+        b.row[b.count] = table->dev_row[i];
+        if (++b.count == kBindPerLaunch) {
+            hipLaunchKernelGGL(set_grad_out_kernel, dim3(1), dim3(kBindPerLaunch), 0, s, table->gout, b);
+            rc = launch_status();
+            if (rc) return rc;
+            b.count = 0;
+        }
+    }
+    if (b.count) {
+        hipLaunchKernelGGL(set_grad_out_kernel, dim3(1), dim3(kBindPerLaunch), 0, s, table->gout, b);
+        rc = launch_status();
+        if (rc) return rc;
+    }
+    table->gout_rows = set;
     return Z1_OK;
 }
 
@@ -1016,16 +1071,21 @@ static int adam_launch(const z1_table* table, int64_t chunk_begin, int64_t chunk
     size_t lds = 0;
     rc = occupancy_lds(dev, kAdamWgPerCu, &lds);
     if (rc) return rc;
-#define Z1_LAUNCH_ADAM(GDT, MODE)                                                                              \
-    hipLaunchKernelGGL((adam_cast_kernel<GDT, MODE>), grid, dim3(kWave * kAdamWaves), lds, s, table->rows,    \
-                       table->chunk_row, chunk_begin, chunk_end, factor, bc, k)
+#define Z1_LAUNCH_ADAM(GDT, MODE, GOUT)                                                                        \
+    hipLaunchKernelGGL((adam_cast_kernel<GDT, MODE, GOUT>), grid, dim3(kWave * kAdamWaves), lds, s, table->rows, \
+                       table->chunk_row, chunk_begin, chunk_end, factor, bc, k, table->gout)
+#define Z1_LAUNCH_ADAM_MODES(GDT, GOUT)                                                                        \
+    if (mode == 1) Z1_LAUNCH_ADAM(GDT, 1, GOUT);                                                              \
+    else Z1_LAUNCH_ADAM(GDT, 0, GOUT)
+    const bool gout = table->gout_rows > 0;
     if (table->g_dtype == Z1_F32) {
-        if (mode == 1) Z1_LAUNCH_ADAM(Z1_F32, 1);
-        else Z1_LAUNCH_ADAM(Z1_F32, 0);
+        if (gout) { Z1_LAUNCH_ADAM_MODES(Z1_F32, true); }
+        else { Z1_LAUNCH_ADAM_MODES(Z1_F32, false); }
     } else {
-        if (mode == 1) Z1_LAUNCH_ADAM(Z1_BF16, 1);
-        else Z1_LAUNCH_ADAM(Z1_BF16, 0);
+        if (gout) { Z1_LAUNCH_ADAM_MODES(Z1_BF16, true); }
+        else { Z1_LAUNCH_ADAM_MODES(Z1_BF16, false); }
     }
+#undef Z1_LAUNCH_ADAM_MODES
 #undef Z1_LAUNCH_ADAM
     return launch_status();
 }

@@ -48,6 +48,7 @@ using OptTensor = std::optional<Tensor>;
 struct Api {
     decltype(&::z1_table_set_grads) table_set_grads;
     decltype(&::z1_table_rebind) table_rebind;
+    decltype(&::z1_table_set_grad_out) table_set_grad_out;
     decltype(&::z1_owner_sum_bf16) owner_sum_bf16;
     decltype(&::z1_owner_sum_workspace) owner_sum_workspace;
     decltype(&::z1_owner_sum_update) owner_sum_update;
@@ -154,8 +155,8 @@ struct TableState {
     std::vector<int64_t> sizes;
     std::vector<int64_t> offsets;                    // flat form: element offset of each row in its buffers
     int64_t flat_need = 0;                           // flat form: elements a buffer must hold
-    std::vector<std::array<uintptr_t, 5>> bound;     // (g, p, m, v, p16) per row, as the device table holds them
-};
+    std::vector<std::array<uintptr_t, 6>> bound;     // (g, p, m, v, p16, FP32 gradient output) per row, as the
+};                                                   // device table holds them
 
 std::unordered_map<uintptr_t, TableState> g_tables;
 
@@ -170,6 +171,9 @@ at::ScalarType column_dtype(const TableState& t, int k) {
     return k == 4 ? at::kBFloat16 : at::kFloat;
 }
 
+// Columns that may be left empty: the BF16 copies (4) and the FP32 gradient outputs (5).
+bool optional_column(int k) { return k >= 4; }
+
 void check_member(const TableState& t, const Tensor& x, at::ScalarType dt, const char* what) {
     require_gpu(x, what);
     TORCH_CHECK(x.device().index() == t.device, what, ": a tensor is on another device than its table");
@@ -177,14 +181,14 @@ void check_member(const TableState& t, const Tensor& x, at::ScalarType dt, const
                 " tensors");
 }
 
-// Per-row addresses of stream k (0 g, 1 p, 2 m, 3 v, 4 p16) for the tensors of a call.
+// Per-row addresses of stream k (0 g, 1 p, 2 m, 3 v, 4 p16, 5 FP32 gradient output) for the tensors of a call.
 void column(const TableState& t, TensorList lst, int k, const char* what, std::vector<uintptr_t>& col) {
     const size_t nr = t.sizes.size();
     const at::ScalarType dt = column_dtype(t, k);
     col.assign(nr, 0);
     if (lst.empty()) {
-        TORCH_CHECK(k == 4, what, ": a gradient, master or moment list is empty");
-        return;                                       // no BF16 copies
+        TORCH_CHECK(optional_column(k), what, ": a gradient, master or moment list is empty");
+        return;                                       // no BF16 copies / no gradient outputs
     }
     if (t.flat) {
         TORCH_CHECK(lst.size() == 1, what, ": a flat table takes one buffer per stream");
@@ -200,7 +204,7 @@ void column(const TableState& t, TensorList lst, int k, const char* what, std::v
     TORCH_CHECK(lst.size() == nr, what, ": expected one tensor per table row (", nr, "), got ", lst.size());
     for (size_t i = 0; i < nr; ++i) {
         const Tensor& x = lst[i];
-        if (k == 4 && x.numel() == 0) continue;      // no BF16 copy for this row
+        if (optional_column(k) && x.numel() == 0) continue;      // none for this row
         check_member(t, x, dt, what);
         TORCH_CHECK(x.numel() == t.sizes[i], what, ": row ", i, " has ", x.numel(), " elements, the table ",
                     t.sizes[i]);
@@ -208,16 +212,19 @@ void column(const TableState& t, TensorList lst, int k, const char* what, std::v
     }
 }
 
-// Points the device table at the call's tensors (streams not given keep their binding), enqueuing a rebind on the
-// stream only when an address moved.
-void bind(TableState& t, TensorList g, const TensorList* pmv16, const char* what, void* stream) {
+// Points the device table at the call's tensors, enqueuing a rebind on the stream only when an address moved.
+// pmv16: the p, m, v, p16 lists, or nullptr to keep their binding; gout: the FP32 gradient outputs (an empty list:
+// none), or nullptr to keep them (the norm reads no output).
+void bind(TableState& t, TensorList g, const TensorList* pmv16, const TensorList* gout, const char* what,
+          void* stream) {
     const size_t nr = t.sizes.size();
     if (nr == 0) return;
-    thread_local std::vector<uintptr_t> cols[5];
+    thread_local std::vector<uintptr_t> cols[6];
     column(t, g, 0, what, cols[0]);
-    for (int k = 1; k < 5; ++k) {
-        if (pmv16) {
-            column(t, pmv16[k - 1], k, what, cols[k]);
+    for (int k = 1; k < 6; ++k) {
+        const TensorList* given = k < 5 ? (pmv16 ? &pmv16[k - 1] : nullptr) : gout;
+        if (given) {
+            column(t, *given, k, what, cols[k]);
         } else {
             cols[k].resize(nr);
             for (size_t i = 0; i < nr; ++i) cols[k][i] = t.bound[i][k];
@@ -228,18 +235,18 @@ void bind(TableState& t, TensorList g, const TensorList* pmv16, const char* what
             TORCH_CHECK(t.sizes[i] == 0 || (cols[1][i] && cols[2][i] && cols[3][i]), what,
                         ": the table updates masters and moments; every row needs p, m and v");
     }
-    bool moved = false, others = false;
+    bool moved = false, others = false, outs = false;
     for (size_t i = 0; i < nr; ++i) {
         moved |= cols[0][i] != t.bound[i][0];
         for (int k = 1; k < 5; ++k) others |= cols[k][i] != t.bound[i][k];
+        outs |= cols[5][i] != t.bound[i][5];
     }
-    if (!moved && !others) return;
-    if (!others) {
+    if (moved && !others) {
         thread_local std::vector<const void*> gp;
         gp.assign(nr, nullptr);
         for (size_t i = 0; i < nr; ++i) gp[i] = reinterpret_cast<const void*>(cols[0][i]);
         check_rc(api().table_set_grads(t.h, gp.data(), static_cast<int>(nr), stream), "z1_table_set_grads");
-    } else {
+    } else if (others) {
         thread_local std::vector<z1_tensor> rows;
         rows.resize(nr);
         for (size_t i = 0; i < nr; ++i) {
@@ -252,8 +259,19 @@ void bind(TableState& t, TensorList g, const TensorList* pmv16, const char* what
         }
         check_rc(api().table_rebind(t.h, rows.data(), static_cast<int>(nr), stream), "z1_table_rebind");
     }
+    if (outs) {
+        bool any = false;
+        thread_local std::vector<float*> op;
+        op.assign(nr, nullptr);
+        for (size_t i = 0; i < nr; ++i) {
+            op[i] = reinterpret_cast<float*>(cols[5][i]);
+            any |= op[i] != nullptr;
+        }
+        check_rc(api().table_set_grad_out(t.h, any ? op.data() : nullptr, static_cast<int>(nr), stream),
+                 "z1_table_set_grad_out");
+    }
     for (size_t i = 0; i < nr; ++i)
-        for (int k = 0; k < 5; ++k) t.bound[i][k] = cols[k][i];
+        for (int k = 0; k < 6; ++k) t.bound[i][k] = cols[k][i];
 }
 
 // A table operator's frame: the registry lock, the table, its device current, torch's current stream there.
@@ -278,7 +296,7 @@ struct OnDevice {
 void grad_sumsq_(int64_t table, TensorList g, const Tensor& partials) {
     double* part = partials_ptr(partials, "grad_sumsq");
     OnTable on(table);
-    bind(on.t, g, nullptr, "grad_sumsq", on.stream);
+    bind(on.t, g, nullptr, nullptr, "grad_sumsq", on.stream);
     check_rc(api().grad_sumsq(on.t.h, part, on.stream), "z1_grad_sumsq");
 }
 
@@ -298,7 +316,7 @@ void grad_norm_clip_(int64_t table, TensorList g, const Tensor& partials, const 
     z1_update_scalars u = scalars("grad_norm_clip", factor, factor_value, norm, grad_norm, std::nullopt, std::nullopt,
                                   std::nullopt, 1.0, max_norm);
     OnTable on(table);
-    bind(on.t, g, nullptr, "grad_norm_clip", on.stream);
+    bind(on.t, g, nullptr, nullptr, "grad_norm_clip", on.stream);
     check_rc(api().grad_update_scalars(on.t.h, part, &u, on.stream), "z1_grad_norm_clip");
 }
 
@@ -321,7 +339,7 @@ void grad_update_scalars_(int64_t table, TensorList g, const Tensor& partials, c
     z1_update_scalars u = scalars("grad_update_scalars", factor, factor_value, norm, grad_norm, flags, clip_log,
                                   sample_size, numer, max_norm);
     OnTable on(table);
-    bind(on.t, g, nullptr, "grad_update_scalars", on.stream);
+    bind(on.t, g, nullptr, nullptr, "grad_update_scalars", on.stream);
     check_rc(api().grad_update_scalars(on.t.h, part, &u, on.stream), "z1_grad_update_scalars");
 }
 
@@ -336,9 +354,12 @@ void clip_factor_(const Tensor& norm, const OptTensor& factor, const OptTensor& 
 }
 
 // ------------------------------------------------------------------------------------------ Adam + BF16
-void adam_cast_(int64_t table, TensorList g, TensorList p, TensorList m, TensorList v, TensorList p16,
-                const OptTensor& factor, double lr, double beta1, double beta2, double eps, double bc1, double bc2,
-                double weight_decay, int64_t adam_mode, int64_t row_begin, int64_t row_end) {
+// Adam + BF16 over rows [row_begin, row_end); with g32 (one FP32 tensor per row, or one flat buffer; an empty
+// list: none) the launch also writes each element's g' = fp32(g * factor) there.
+void adam_cast_impl(int64_t table, TensorList g, TensorList p, TensorList m, TensorList v, TensorList p16,
+                    TensorList g32, const OptTensor& factor, double lr, double beta1, double beta2, double eps,
+                    double bc1, double bc2, double weight_decay, int64_t adam_mode, int64_t row_begin,
+                    int64_t row_end) {
     float* fac = scalar_ptr(factor, "adam_cast");
     OnTable on(table);
     TableState& t = on.t;
@@ -347,7 +368,7 @@ void adam_cast_(int64_t table, TensorList g, TensorList p, TensorList m, TensorL
     TORCH_CHECK(0 <= row_begin && row_begin <= row_end && row_end <= nr, "yoco_z1: rows [", row_begin, ", ", row_end,
                 ") outside the table's ", nr, " rows");
     const TensorList rest[4] = {p, m, v, p16};
-    bind(t, g, rest, "adam_cast", on.stream);
+    bind(t, g, rest, &g32, "adam_cast", on.stream);
     if (row_begin == 0 && row_end == nr) {
         check_rc(api().adam_cast(t.h, fac, static_cast<float>(lr), static_cast<float>(beta1),
                                  static_cast<float>(beta2), static_cast<float>(eps), static_cast<float>(bc1),
@@ -362,6 +383,21 @@ void adam_cast_(int64_t table, TensorList g, TensorList p, TensorList m, TensorL
     }
 }
 
+void adam_cast_(int64_t table, TensorList g, TensorList p, TensorList m, TensorList v, TensorList p16,
+                const OptTensor& factor, double lr, double beta1, double beta2, double eps, double bc1, double bc2,
+                double weight_decay, int64_t adam_mode, int64_t row_begin, int64_t row_end) {
+    adam_cast_impl(table, g, p, m, v, p16, TensorList(), factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay,
+                   adam_mode, row_begin, row_end);
+}
+
+void adam_cast_gout_(int64_t table, TensorList g, TensorList p, TensorList m, TensorList v, TensorList p16,
+                     TensorList g32, const OptTensor& factor, double lr, double beta1, double beta2, double eps,
+                     double bc1, double bc2, double weight_decay, int64_t adam_mode, int64_t row_begin,
+                     int64_t row_end) {
+    adam_cast_impl(table, g, p, m, v, p16, g32, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, adam_mode,
+                   row_begin, row_end);
+}
+
 void adam_cast_dev_(int64_t table, TensorList g, TensorList p, TensorList m, TensorList v, TensorList p16,
                     const OptTensor& factor, const Tensor& bc, double lr, double beta1, double beta2, double eps,
                     double weight_decay, int64_t adam_mode) {
@@ -373,7 +409,8 @@ void adam_cast_dev_(int64_t table, TensorList g, TensorList p, TensorList m, Ten
     TableState& t = on.t;
     TORCH_CHECK(t.has_pmv, "yoco_z1: adam_cast_dev needs a table with p, m and v");
     const TensorList rest[4] = {p, m, v, p16};
-    bind(t, g, rest, "adam_cast_dev", on.stream);
+    const TensorList none;
+    bind(t, g, rest, &none, "adam_cast_dev", on.stream);
     check_rc(api().adam_cast_dev(t.h, fac, static_cast<float>(lr), static_cast<float>(beta1),
                                  static_cast<float>(beta2), static_cast<float>(eps),
                                  static_cast<const float*>(bc.data_ptr()), static_cast<float>(weight_decay),
@@ -551,8 +588,8 @@ void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
 
 const char* const kOps[] = {
     "grad_sumsq_", "norm_clip_", "grad_norm_clip_", "update_scalars_", "grad_update_scalars_", "clip_factor_",
-    "adam_cast_", "adam_cast_dev_", "bias_corrections_step_", "owner_sum_", "owner_sum_update_", "sum_slots_",
-    "scale_up_", "cast_bf16_", "embedding_dense_backward_out_", "embedding_dense_backward",
+    "adam_cast_", "adam_cast_gout_", "adam_cast_dev_", "bias_corrections_step_", "owner_sum_", "owner_sum_update_",
+    "sum_slots_", "scale_up_", "cast_bf16_", "embedding_dense_backward_out_", "embedding_dense_backward",
 };
 
 }  // namespace
@@ -574,6 +611,9 @@ TORCH_LIBRARY(yoco_z1, m) {
     m.def("adam_cast_(int table, Tensor[] g, Tensor(a2!)[] p, Tensor(a3!)[] m, Tensor(a4!)[] v, "
           "Tensor(a5!)[] p16, Tensor? factor, float lr, float beta1, float beta2, float eps, float bc1, float bc2, "
           "float weight_decay, int adam_mode, int row_begin, int row_end) -> ()");
+    m.def("adam_cast_gout_(int table, Tensor[] g, Tensor(a2!)[] p, Tensor(a3!)[] m, Tensor(a4!)[] v, "
+          "Tensor(a5!)[] p16, Tensor(a6!)[] g32, Tensor? factor, float lr, float beta1, float beta2, float eps, "
+          "float bc1, float bc2, float weight_decay, int adam_mode, int row_begin, int row_end) -> ()");
     m.def("adam_cast_dev_(int table, Tensor[] g, Tensor(a2!)[] p, Tensor(a3!)[] m, Tensor(a4!)[] v, "
           "Tensor(a5!)[] p16, Tensor? factor, Tensor bc, float lr, float beta1, float beta2, float eps, "
           "float weight_decay, int adam_mode) -> ()");
@@ -603,6 +643,7 @@ TORCH_LIBRARY_IMPL(yoco_z1, CUDA, m) {
     m.impl("grad_update_scalars_", &grad_update_scalars_);
     m.impl("clip_factor_", &clip_factor_);
     m.impl("adam_cast_", &adam_cast_);
+    m.impl("adam_cast_gout_", &adam_cast_gout_);
     m.impl("adam_cast_dev_", &adam_cast_dev_);
     m.impl("bias_corrections_step_", &bias_corrections_step_);
     m.impl("owner_sum_", &owner_sum_);
@@ -633,6 +674,7 @@ int z1t_init(const char* path) {
     if (!a.field) return -2;
     Z1T_RESOLVE(table_set_grads, z1_table_set_grads)
     Z1T_RESOLVE(table_rebind, z1_table_rebind)
+    Z1T_RESOLVE(table_set_grad_out, z1_table_set_grad_out)
     Z1T_RESOLVE(owner_sum_bf16, z1_owner_sum_bf16)
     Z1T_RESOLVE(owner_sum_workspace, z1_owner_sum_workspace)
     Z1T_RESOLVE(owner_sum_update, z1_owner_sum_update)
@@ -674,7 +716,7 @@ int z1t_table_register(z1_table* table, int device, int g_dtype, int has_pmv, in
         t.sizes[i] = rows[i].n;
         t.bound[i] = {reinterpret_cast<uintptr_t>(rows[i].g), reinterpret_cast<uintptr_t>(rows[i].p),
                       reinterpret_cast<uintptr_t>(rows[i].m), reinterpret_cast<uintptr_t>(rows[i].v),
-                      reinterpret_cast<uintptr_t>(rows[i].p16)};
+                      reinterpret_cast<uintptr_t>(rows[i].p16), 0};          // no gradient outputs yet
     }
     if (t.flat) {
         t.offsets.assign(offsets, offsets + nrows);

@@ -9,9 +9,12 @@ arguments, and collects in ``.cast`` the addresses of the masters whose BF16 cop
   * what a parameter list needs -- its table, the BF16 destinations found in ``dest``, the masters they belong to
     -- is worked out once per list of masters (keyed by their addresses and sizes, as ``dest`` is keyed by
     address) and reused while the list recurs; each call's tensors are still checked, by the operator;
-  * ``fold`` / ``fold_factor`` (set by zero1_fast.step under YOCO_Z1_FOLD_SCALE=1) name masters whose BF16 gradient
-    the kernel reads times the factor, in place of the FP32 gradient a scale pass would have written: the same
-    products g' = fp32(float(g16) * factor), 6 bytes per element less traffic.
+  * ``fold`` / ``fold_factor`` (set by zero1_fast.step with the fused Adam) name masters whose BF16 gradient the
+    kernel reads times the factor, in place of the FP32 gradient a scale pass would have written first: the same
+    products g' = fp32(float(g16) * factor).  With ``fold_writes`` (zero1_fast's default) the kernel also stores
+    g' into the FP32 gradient tensors of the call, so they end as the reference's scale pass leaves them, in one
+    pass of 32 bytes per element instead of 6 + 30; without it (YOCO_Z1_FOLD_SCALE=1) they are left as they were
+    (28 bytes per element).
 ``scale_up`` keeps ``fused_adam_cast.py:84-89``'s signature.
 """
 from collections import OrderedDict
@@ -32,6 +35,7 @@ class FusedAdamCast:
         self.cast = set()                 # masters whose BF16 copy was written since the caller last cleared it
         self.fold = {}                    # master address -> BF16 gradient read in place of the FP32 one
         self.fold_factor = None           # the 1-element fp32 device factor of the folded gradients
+        self.fold_writes = False          # folded rows also write g' into the call's FP32 gradient tensors
         self._tables = ops.TableCache()
         self._plans = OrderedDict()       # masters' (address, size)s -> (table, BF16 destinations, addresses)
 
@@ -54,6 +58,7 @@ class FusedAdamCast:
             self.cast.update(written)
             return
         groups = {False: [], True: []}    # rows reading the FP32 gradient / a folded BF16 one
+        outs = []                         # the folded rows' FP32 gradients (written when fold_writes)
         written = []
         for g, p, m, v in zip(*tensor_lists):
             n, d = self._row(g, p, m, v)
@@ -64,13 +69,16 @@ class FusedAdamCast:
             if g16 is not None and (g16.dtype != torch.bfloat16 or not g16.is_contiguous() or g16.numel() != n):
                 raise RuntimeError('fused_adam_cast: a folded gradient must be contiguous bf16')
             groups[g16 is not None].append((g if g16 is None else g16, p, m, v, d, n))
+            if g16 is not None:
+                outs.append(g)
         if groups[True] and self.fold_factor is None:
             raise RuntimeError('fused_adam_cast: folded gradients without a factor')
         for folded, rows in groups.items():
             if rows:
                 table = self._tables.get(rows, rows[0][1].device)
                 ops.adam_cast(table, self.fold_factor if folded else None, lr, beta1, beta2, eps, bc1, bc2,
-                              weight_decay, int(mode), tensors=ops.rows_lists(rows))
+                              weight_decay, int(mode), tensors=ops.rows_lists(rows),
+                              g32=outs if folded and self.fold_writes else None)
         self.cast.update(written)
 
     def _row(self, g, p, m, v):

@@ -86,22 +86,28 @@ def clip_factor(norm, factor=1.0, grad_norm_out=None, factor_out=None, max_norm=
 
 
 # ------------------------------------------------------------------------------------------------ Adam + BF16
-def adam_cast(table, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode, tensors=None):
+def adam_cast(table, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode, tensors=None, g32=None):
     """One multi-tensor Adam + BF16 launch over the table.  factor: 1-element fp32 device tensor or None.
-    tensors: (g, p, m, v, p16) lists, by default the table's bound tensors."""
-    adam_cast_rows(table, 0, table.nrows, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode, tensors)
+    tensors: (g, p, m, v, p16) lists, by default the table's bound tensors.  g32: FP32 gradient outputs (one per
+    row, an empty tensor for none, or the flat buffer): the launch also writes g' = fp32(g * factor) there, the
+    master gradient the reference's scale pass writes (yoco/tasks/zero1_fast.py:175-192)."""
+    adam_cast_rows(table, 0, table.nrows, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode, tensors, g32)
 
 
 def adam_cast_rows(table, row_begin, row_end, factor, lr, beta1, beta2, eps, bc1, bc2, weight_decay, mode,
-                   tensors=None):
+                   tensors=None, g32=None):
     """adam_cast over the table rows [row_begin, row_end) only (indices of the rows the table was built from)."""
     if not 0 <= int(row_begin) <= int(row_end) <= table.nrows:
         raise RuntimeError(f'yoco_z1: rows [{row_begin}, {row_end}) outside the table\'s {table.nrows} rows')
     if table.numel == 0 or row_begin == row_end:
         return                                           # nothing to update (and no tensor to dispatch on)
     g, p, m, v, p16 = _bound(table) if tensors is None else tensors
-    _OPS.adam_cast_(table.handle_int, g, p, m, v, p16, factor, f32(lr), f32(beta1), f32(beta2), f32(eps), f32(bc1),
-                    f32(bc2), f32(weight_decay), int(mode), int(row_begin), int(row_end))
+    args = (factor, f32(lr), f32(beta1), f32(beta2), f32(eps), f32(bc1), f32(bc2), f32(weight_decay), int(mode),
+            int(row_begin), int(row_end))
+    if g32 is None:
+        _OPS.adam_cast_(table.handle_int, g, p, m, v, p16, *args)
+    else:
+        _OPS.adam_cast_gout_(table.handle_int, g, p, m, v, p16, list(g32), *args)
 
 
 def adam_cast_dev(table, factor, lr, beta1, beta2, eps, bc, weight_decay, mode, tensors=None):

@@ -4,10 +4,12 @@ norm, clip, gradient scale and Adam + BF16 copy on this build's gfx950 operators
 Switches, read at import like the reference's (yoco/tasks/zero1_fast.py:23-44; off unless set to 1):
     YOCO_ZERO1_FAST, YOCO_ZERO1_ALLGATHER, YOCO_ZERO1_PARAM_VIEWS, YOCO_PARAM_ALLREDUCE + YOCO_GRAD_REDUCE_OWNER,
     YOCO_Z1_ONE_PASS, YOCO_Z1_SCALE_KERNEL, YOCO_FUSED_ADAM, YOCO_CE_ALLGATHER (refused: not part of this build)
-plus one of this build, YOCO_Z1_FOLD_SCALE (off by default): with the fused Adam, the Adam kernel reads each owned
-BF16 gradient times the factor itself instead of the FP32 master gradient a scale pass would write first -- the
-same products, 6 bytes per element less traffic, but the masters' ``.grad`` tensors are then left as they were.
-By default the step writes them (g32 = fp32(g16 * factor)) as the reference does.
+plus one of this build, YOCO_Z1_FOLD_SCALE (off by default).  With the fused Adam, the Adam kernel reads each owned
+BF16 gradient times the factor itself instead of the FP32 master gradient a scale pass writes first -- the same
+products g32 = fp32(g16 * factor).  By default it also writes them into the masters' ``.grad`` tensors, as the
+reference's scale pass does (one pass of 32 bytes per element instead of 6 + 30, one launch instead of one per
+tensor plus one); with YOCO_Z1_FOLD_SCALE=1 it does not (28 bytes per element), and the masters' ``.grad`` tensors
+are left as they were.  Without the fused Adam the scale pass runs as in the reference.
 
 Imported with YOCO_ZERO1_FAST=1 where fairseq is importable, the module installs itself on fairseq's
 ``_FP16OptimizerMixin`` (``clip_grad_norm`` / ``step`` / ``zero_grad``), adds the parameter placement to the
@@ -226,9 +228,10 @@ def step(self, closure=None, groups=None):
     if plan.mine:
         f1 = _device_factor(self._multiply_factor, plan.mine[0][1].device)
         folded = {}
-        if plan.fused is not None and FOLD_SCALE:
+        if plan.fused is not None:
             folded = {b.data_ptr(): a.grad for a, b, _ in plan.mine
-                      if a.grad.dtype == torch.bfloat16 and a.grad.is_contiguous() and a.grad.numel() == b.numel()}
+                      if a.grad.dtype == torch.bfloat16 and a.grad.is_contiguous() and a.grad.numel() == b.numel()
+                      and (FOLD_SCALE or b.grad.is_contiguous())}
         for a, b, _ in plan.mine:
             if b.data_ptr() in folded:
                 continue
@@ -237,14 +240,14 @@ def step(self, closure=None, groups=None):
             else:
                 torch.mul(a.grad, f1, out=b.grad)
         if plan.fused is not None:
-            plan.fused.fold, plan.fused.fold_factor = folded, f1
+            plan.fused.fold, plan.fused.fold_factor, plan.fused.fold_writes = folded, f1, not FOLD_SCALE
     self._multiply_factor = 1.0
     self._needs_sync = False
     try:
         self.fp32_optimizer.step(closure, groups=groups)
     finally:
         if plan.fused is not None:
-            plan.fused.fold, plan.fused.fold_factor = {}, None
+            plan.fused.fold, plan.fused.fold_factor, plan.fused.fold_writes = {}, None, False
     written = plan.fused.cast if plan.fused is not None else set()
     for _, b, view in plan.mine:
         if b.data_ptr() not in written:

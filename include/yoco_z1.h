@@ -79,6 +79,17 @@ int z1_table_info(const z1_table* table, int64_t* numel, int64_t* nchunks, int* 
  * element-wise path. */
 int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* stream);
 
+/* Gives the table FP32 gradient outputs: g32 is a HOST array of nrows device float pointers, one per row given to
+ * z1_table_create (entries of empty rows are ignored; NULL: no output for that row), or g32 = NULL for none.  The
+ * z1_adam_cast, z1_adam_cast_rows and z1_adam_cast_dev launches enqueued after it also store every element's
+ * g' = fp32(g * factor), the value the update consumes, to its row's output: the FP32 master gradient that the
+ * reference's scale pass writes before its Adam reads it back (yoco/tasks/zero1_fast.py:175-192 with
+ * yoco/tasks/fused_adam_cast.py:75-89), here written by the one pass that reads the BF16 gradient (32 bytes per
+ * element instead of 6 + 30 over two passes, and one launch instead of one per tensor plus one).  No counterpart in
+ * the reference: a fusion of two of its passes with the same values.  Outputs must not overlap any row's p, m, v or
+ * p16.  Enqueued on the stream like a launch; no allocation, no host synchronisation. */
+int z1_table_set_grad_out(z1_table* table, float* const* g32, int nrows, void* stream);
+
 /* Points every row of the table at new tensors: rows as given to z1_table_create (the same count and the same n per
  * row, else Z1_E_SIZE; p, m, v present wherever the table had them).  Enqueued on the stream like z1_table_set_grads
  * (no allocation, no host synchronisation).  For callers whose tensors move as a whole -- a framework that runs the

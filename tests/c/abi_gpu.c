@@ -11,7 +11,10 @@
  *      1e-6 of the average's exact norm; z1_owner_sum_update (with the clip chain, twice, then on a shorter
  *      input with the same workspace) gives the same bits as z1_owner_sum_bf16 + z1_norm_clip;
  *   3. the embedding gradient (workspace query, ids with repeats, out-of-range ids and padding, x 1/8 after) at
- *      5000 rows (aten's sort-path order) and 1000 rows (its order for few indices): bit-exact.
+ *      5000 rows (aten's sort-path order) and 1000 rows (its order for few indices): bit-exact;
+ *   4. a BF16-gradient table with FP32 gradient outputs (z1_table_set_grad_out; one output off the vector alignment,
+ *      one row without): Adam + BF16 bit-exact, every output the oracle's scale_up bit for bit; with the outputs
+ *      removed, a second launch leaves them untouched.
  * Built by __graft_entry__.build() with gcc, linked against libyoco_z1.so, the oracle and the HIP runtime, twice:
  * as tests/c/libabi_gpu.so, whose abi_gpu_run() tests/test_gpu_c_abi.py calls in-process, and with -DABI_GPU_MAIN
  * as the standalone program tests/c/abi_gpu.  Returns (exits with) 0 and prints "ok" on success. */
@@ -27,6 +30,7 @@
 
 /* oracle/z1_oracle.c */
 uint16_t oracle_bf16_rne(float x);
+void oracle_scale_up(const uint16_t* g16, float* g32, float factor, int64_t n);
 void oracle_owner_sum(const uint16_t* const* src, int world, int64_t n, float scale, uint16_t* out, float* out_sum);
 double oracle_sumsq_f32(const float* g, int64_t n);
 double oracle_sumsq_bf16(const uint16_t* g, int64_t n);
@@ -330,11 +334,100 @@ static int embedding_grad(int64_t R) {
     return 0;
 }
 
+static int gradient_outputs(void) {
+    enum { R = 3 };
+    const int64_t sizes[R] = {4096 + 13, 777, 256 * 5};
+    const int64_t off[R] = {0, 4160, 4992};                 /* 64-element aligned rows */
+    const int64_t total = 4992 + 256 * 5;
+    uint16_t *hg = malloc(total * 2), *h16 = malloc(total * 2), *o16 = malloc(total * 2);
+    float *hp = malloc(total * 4), *hm = malloc(total * 4), *hv = malloc(total * 4);
+    float *op = malloc(total * 4), *om = malloc(total * 4), *ov = malloc(total * 4);
+    float *hout = malloc((total + 1) * 4), *oout = malloc((total + 1) * 4), *ref = malloc(total * 4);
+    for (int64_t i = 0; i < total; ++i) {
+        hg[i] = oracle_bf16_rne(normal(1e-2));
+        hp[i] = normal(0.02);
+        hm[i] = normal(1e-4);
+        hv[i] = fabsf(normal(1e-8));
+    }
+    for (int64_t i = 0; i <= total; ++i) hout[i] = -7.0f;
+    uint16_t *dg, *d16;
+    float *dp, *dm, *dv, *dout, *dfac;
+    HIP_OK(hipMalloc((void**)&dg, total * 2));
+    HIP_OK(hipMalloc((void**)&d16, total * 2));
+    HIP_OK(hipMalloc((void**)&dp, total * 4));
+    HIP_OK(hipMalloc((void**)&dm, total * 4));
+    HIP_OK(hipMalloc((void**)&dv, total * 4));
+    HIP_OK(hipMalloc((void**)&dout, (total + 1) * 4));
+    HIP_OK(hipMalloc((void**)&dfac, 4));
+    HIP_OK(hipMemcpy(dg, hg, total * 2, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dp, hp, total * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dm, hm, total * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dv, hv, total * 4, hipMemcpyHostToDevice));
+    HIP_OK(hipMemcpy(dout, hout, (total + 1) * 4, hipMemcpyHostToDevice));
+    const float fac = 0.37f;
+    HIP_OK(hipMemcpy(dfac, &fac, 4, hipMemcpyHostToDevice));
+    z1_tensor rows[R];
+    for (int i = 0; i < R; ++i) {
+        rows[i].g = dg + off[i];
+        rows[i].p = dp + off[i];
+        rows[i].m = dm + off[i];
+        rows[i].v = dv + off[i];
+        rows[i].p16 = d16 + off[i];
+        rows[i].n = sizes[i];
+    }
+    z1_table* t = NULL;
+    Z1_OK_(z1_table_create(rows, R, Z1_BF16, &t));
+    /* row 0's output one float past its slot (off the 16-byte alignment: element-wise path), row 1 none */
+    float* outs[R] = {dout + off[0] + 1, NULL, dout + off[2]};
+    EXPECT(z1_table_set_grad_out(t, outs, R - 1, NULL) == Z1_E_SIZE);
+    EXPECT(z1_table_set_grad_out(NULL, outs, R, NULL) == Z1_E_NULL);
+    Z1_OK_(z1_table_set_grad_out(t, outs, R, NULL));
+    const float lr = 3e-4f, b1 = 0.9f, b2 = 0.95f, eps = 1e-8f, wd = 0.1f;
+    float bc[2];
+    oracle_bias_corrections(0.9, 0.95, 3, 1, bc);
+    Z1_OK_(z1_adam_cast(t, dfac, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL));
+    HIP_OK(hipDeviceSynchronize());
+    HIP_OK(hipMemcpy(op, dp, total * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(om, dm, total * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(ov, dv, total * 4, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(o16, d16, total * 2, hipMemcpyDeviceToHost));
+    HIP_OK(hipMemcpy(oout, dout, (total + 1) * 4, hipMemcpyDeviceToHost));
+    for (int i = 0; i < R; ++i) {
+        const int64_t o = off[i], n = sizes[i];
+        oracle_adam_cast(hg + o, 1, hp + o, hm + o, hv + o, h16 + o, n, fac, 1, lr, b1, b2, eps, bc[0], bc[1], wd, 1);
+        EXPECT(same_f32(op + o, hp + o, n) && same_f32(om + o, hm + o, n) && same_f32(ov + o, hv + o, n));
+        EXPECT(memcmp(o16 + o, h16 + o, (size_t)n * 2) == 0);
+        oracle_scale_up(hg + o, ref, fac, n);
+        if (i == 0) EXPECT(same_f32(oout + o + 1, ref, n));
+        if (i == 2) EXPECT(same_f32(oout + o, ref, n));
+    }
+    for (int64_t i = off[0] + 1 + sizes[0]; i < off[2]; ++i) EXPECT(bits(oout[i]) == bits(-7.0f));   /* row 1 */
+    EXPECT(bits(oout[0]) == bits(-7.0f) && bits(oout[total]) == bits(-7.0f));
+    Z1_OK_(z1_table_set_grad_out(t, NULL, 0, NULL));        /* outputs removed: the next launch writes none */
+    HIP_OK(hipMemcpy(dout, hout, (total + 1) * 4, hipMemcpyHostToDevice));
+    Z1_OK_(z1_adam_cast(t, dfac, lr, b1, b2, eps, bc[0], bc[1], wd, 1, NULL));
+    HIP_OK(hipDeviceSynchronize());
+    HIP_OK(hipMemcpy(oout, dout, (total + 1) * 4, hipMemcpyDeviceToHost));
+    EXPECT(same_f32(oout, hout, total + 1));
+    Z1_OK_(z1_table_destroy(t));
+    HIP_OK(hipFree(dg));
+    HIP_OK(hipFree(d16));
+    HIP_OK(hipFree(dp));
+    HIP_OK(hipFree(dm));
+    HIP_OK(hipFree(dv));
+    HIP_OK(hipFree(dout));
+    HIP_OK(hipFree(dfac));
+    free(hg); free(h16); free(o16); free(hp); free(hm); free(hv); free(op); free(om); free(ov);
+    free(hout); free(oout); free(ref);
+    return 0;
+}
+
 int abi_gpu_run(void) {
     int rc = table_update();
     if (rc == 0) rc = owner_sum();
     if (rc == 0) rc = embedding_grad(5000);
     if (rc == 0) rc = embedding_grad(1000);
+    if (rc == 0) rc = gradient_outputs();
     printf("%s\n", rc ? "FAIL" : "ok");
     fflush(stdout);
     return rc;

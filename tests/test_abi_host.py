@@ -71,6 +71,7 @@ def test_argument_errors_without_device_work(pkg):
     assert L.z1_grad_norm_clip(None, None, None, 1.0, None, None, None, 1.0, None) == -1
     assert L.z1_grad_update_scalars(None, None, None, None) == -1
     assert L.z1_table_set_grads(None, None, 0, None) == -1
+    assert L.z1_table_set_grad_out(None, None, 0, None) == -1
     u = _lib.Z1UpdateScalars()
     assert L.z1_owner_sum_update(ctypes.cast(arr, ctypes.c_void_p), 1, 10, 1.0, ctypes.c_void_p(32), None, None,
                                  ctypes.byref(u), None) == -1                      # no workspace

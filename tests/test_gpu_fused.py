@@ -214,3 +214,52 @@ def test_operators_follow_moved_state_tensors(pkg, dev):
         Y.adam_cast_(table.handle_int, [g[0][1:]] + g[1:], p, m, v, p16, *args)
     with pytest.raises(RuntimeError, match='rows \\[0, 9\\) outside'):
         Y.adam_cast_(table.handle_int, g, p, m, v, p16, *args[:-1], 9)
+
+
+@pytest.mark.parametrize('mode', [1, 0])
+def test_adam_writes_the_scaled_gradients(pkg, dev, mode):
+    """adam_cast with FP32 gradient outputs (z1_table_set_grad_out): BF16 gradients read times the factor, every
+    output row holding fp32(float(g16) * factor) bit for bit as the scale pass writes it, and m / v / master / BF16
+    copy as scale pass + Adam give them.  Rows: aligned, an output off the 16-byte alignment (element-wise path), a
+    row without an output, an empty row, tails.  A later launch without outputs leaves them untouched."""
+    from faster_yoco_amd import ops
+    sizes = [5000, 256 * 9, 0, 33, 1 << 14]
+    gen = torch.Generator(device='cpu').manual_seed(21 + mode)
+    g16 = [(torch.randn(n, generator=gen) * 1e-2).to(torch.bfloat16).to(dev) for n in sizes]
+    p = [(torch.randn(n, generator=gen) * 0.02).to(dev) for n in sizes]
+    m = [(torch.randn(n, generator=gen) * 1e-4).to(dev) for n in sizes]
+    v = [(torch.randn(n, generator=gen) * 1e-8).abs().to(dev) for n in sizes]
+    p16 = [torch.zeros(n, dtype=torch.bfloat16, device=dev) for n in sizes]
+    raw = torch.full((sum(sizes) + 8,), -7.0, device=dev)
+    outs, off = [], 1                                       # row 1's output is 4 bytes off the vector alignment
+    for i, n in enumerate(sizes):
+        outs.append(torch.empty(0, device=dev) if i == 3 else raw[off:off + n])
+        off += n
+    outs[0] = torch.full((sizes[0],), -7.0, device=dev)     # row 0: an aligned output of its own
+    keep = [(g.view(torch.int16).cpu().numpy().view(np.uint16).copy(), a.cpu().numpy().copy(),
+             b.cpu().numpy().copy(), c.cpu().numpy().copy()) for g, a, b, c in zip(g16, p, m, v)]
+    factor = torch.tensor([0.37], device=dev)
+    fac = float(factor.item())
+    table = ops.Table([r + (r[0].numel(),) for r in zip(g16, p, m, v, p16)], dev)
+    hp = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    bc1, bc2 = ops.bias_corrections(hp['beta1'], hp['beta2'], 7)
+    ops.adam_cast(table, factor, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2, hp['weight_decay'], mode,
+                  g32=outs)
+    torch.cuda.synchronize()
+    for i, (gb, p0, m0, v0) in enumerate(keep):
+        po, mo, vo, p16o = oracle.adam_cast(gb, p0, m0, v0, step=7, mode=mode, factor=fac, **hp)
+        assert np.array_equal(f32_bits(p[i]), po.view(np.uint32)), i
+        assert np.array_equal(f32_bits(m[i]), mo.view(np.uint32)), i
+        assert np.array_equal(f32_bits(v[i]), vo.view(np.uint32)), i
+        assert np.array_equal(p16[i].view(torch.int16).cpu().numpy().view(np.uint16), p16o), i
+        if i != 3:
+            assert np.array_equal(f32_bits(outs[i]), oracle.scale_up(gb, fac).view(np.uint32)), i
+    assert raw[0].item() == -7.0 and raw[-1].item() == -7.0       # nothing written outside the outputs
+    for o in outs:
+        o.fill_(-7.0)
+    ops.adam_cast(table, factor, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2, hp['weight_decay'], mode)
+    torch.cuda.synchronize()
+    assert all(bool((o == -7.0).all()) for o in outs)              # outputs cleared for a launch without them
+    with pytest.raises(RuntimeError, match='row 0 has 4999 elements'):
+        ops.adam_cast(table, factor, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2, hp['weight_decay'],
+                      mode, g32=[outs[0][1:]] + outs[1:])

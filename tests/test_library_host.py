@@ -21,6 +21,7 @@ MUTATES = {
     'update_scalars_': {'factor', 'norm', 'grad_norm', 'flags', 'clip_log'},
     'grad_update_scalars_': {'partials', 'factor', 'norm', 'grad_norm', 'flags', 'clip_log'},
     'clip_factor_': {'factor', 'grad_norm'}, 'adam_cast_': {'p', 'm', 'v', 'p16'},
+    'adam_cast_gout_': {'p', 'm', 'v', 'p16', 'g32'},
     'adam_cast_dev_': {'p', 'm', 'v', 'p16'}, 'bias_corrections_step_': {'step', 'bc'},
     'owner_sum_': {'out', 'out_sum', 'partials'},
     'owner_sum_update_': {'out', 'workspace', 'out_sum', 'factor', 'norm', 'grad_norm', 'flags', 'clip_log'},
