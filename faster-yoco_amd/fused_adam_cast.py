@@ -6,9 +6,10 @@ an fp32 master -> the BF16 tensor to write), called by fairseq's FusedAdamV2.ste
 arguments, and collects in ``.cast`` the addresses of the masters whose BF16 copy it wrote.  Internally:
   * all the call's tensors go to one ``torch.ops.yoco_z1.adam_cast_`` launch over a table (cached by the rows'
     sizes, bound to the call's tensors), where the reference launches one Triton kernel per tensor;
-  * what a parameter list needs -- its table, the BF16 destinations found in ``dest``, the masters they belong to
-    -- is worked out once per list of masters (keyed by their addresses and sizes, as ``dest`` is keyed by
-    address) and reused while the list recurs; each call's tensors are still checked, by the operator;
+  * what a parameter list needs -- its tables, the BF16 destinations found in ``dest``, the masters they belong to
+    -- is worked out once per list of masters and set of folded rows (keyed by the masters' addresses and sizes,
+    as ``dest`` is keyed by address) and reused while they recur; each call's tensors are still checked, by the
+    operator;
   * ``fold`` / ``fold_factor`` (set by zero1_fast.step with the fused Adam) name masters whose BF16 gradient the
     kernel reads times the factor, in place of the FP32 gradient a scale pass would have written first: the same
     products g' = fp32(float(g16) * factor).  With ``fold_writes`` (zero1_fast's default) the kernel also stores
@@ -37,48 +38,33 @@ class FusedAdamCast:
         self.fold_factor = None           # the 1-element fp32 device factor of the folded gradients
         self.fold_writes = False          # folded rows also write g' into the call's FP32 gradient tensors
         self._tables = ops.TableCache()
-        self._plans = OrderedDict()       # masters' (address, size)s -> (table, BF16 destinations, addresses)
+        # (masters' (address, size)s, which rows are folded) -> (groups, written addresses); a group is
+        # (folded, row indices or None for all rows, table, BF16 destinations)
+        self._plans = OrderedDict()
 
     def __call__(self, chunk_size, noop_flag, tensor_lists, lr, beta1, beta2, eps, step, mode, bias_correction,
                  weight_decay):
         if int(mode) not in (0, 1):
             raise RuntimeError(f'fused_adam_cast: unsupported adam mode {mode}')
         bc1, bc2 = ops.bias_corrections(beta1, beta2, step, bias_correction)
-        if not self.fold:
-            g, p, m, v = tensor_lists
-            if not p:
-                return
-            key = tuple([(t.data_ptr(), t.numel()) for t in p])
-            plan = self._plans.get(key)
-            if plan is None:
-                plan = self._plan(key, tensor_lists)
-            table, p16, written = plan
-            ops.adam_cast(table, None, lr, beta1, beta2, eps, bc1, bc2, weight_decay, int(mode),
-                          tensors=(g, p, m, v, p16))
-            self.cast.update(written)
+        g, p, m, v = tensor_lists
+        if not p:
             return
-        groups = {False: [], True: []}    # rows reading the FP32 gradient / a folded BF16 one
-        outs = []                         # the folded rows' FP32 gradients (written when fold_writes)
-        written = []
-        for g, p, m, v in zip(*tensor_lists):
-            n, d = self._row(g, p, m, v)
-            key = p.data_ptr()
-            if d is not None:
-                written.append(key)
-            g16 = self.fold.get(key)
-            if g16 is not None and (g16.dtype != torch.bfloat16 or not g16.is_contiguous() or g16.numel() != n):
-                raise RuntimeError('fused_adam_cast: a folded gradient must be contiguous bf16')
-            groups[g16 is not None].append((g if g16 is None else g16, p, m, v, d, n))
-            if g16 is not None:
-                outs.append(g)
-        if groups[True] and self.fold_factor is None:
+        key = tuple([(t.data_ptr(), t.numel()) for t in p])
+        g16 = [self.fold.get(a) for a, _ in key] if self.fold else None
+        folded = None if g16 is None else tuple(x is not None for x in g16)
+        if folded is not None and any(folded) and self.fold_factor is None:
             raise RuntimeError('fused_adam_cast: folded gradients without a factor')
-        for folded, rows in groups.items():
-            if rows:
-                table = self._tables.get(rows, rows[0][1].device)
-                ops.adam_cast(table, self.fold_factor if folded else None, lr, beta1, beta2, eps, bc1, bc2,
-                              weight_decay, int(mode), tensors=ops.rows_lists(rows),
-                              g32=outs if folded and self.fold_writes else None)
+        plan = self._plans.get((key, folded))
+        if plan is None:
+            plan = self._plan(key, folded, tensor_lists, g16)
+        groups, written = plan
+        for is_folded, idx, table, p16 in groups:
+            pick = (lambda lst: lst) if idx is None else (lambda lst: [lst[i] for i in idx])
+            gin = pick(g16) if is_folded else pick(g)
+            ops.adam_cast(table, self.fold_factor if is_folded else None, lr, beta1, beta2, eps, bc1, bc2,
+                          weight_decay, int(mode), tensors=(gin, pick(p), pick(m), pick(v), p16),
+                          g32=pick(g) if is_folded and self.fold_writes else None)
         self.cast.update(written)
 
     def _row(self, g, p, m, v):
@@ -94,17 +80,30 @@ class FusedAdamCast:
             raise RuntimeError('fused_adam_cast: the bf16 destination must be a contiguous bf16 view')
         return n, d
 
-    def _plan(self, key, tensor_lists):
-        """Table, BF16 destination list and written addresses for a list of masters (checked row by row)."""
-        rows, written = [], []
-        for g, p, m, v in zip(*tensor_lists):
+    def _plan(self, key, folded, tensor_lists, g16):
+        """Groups (rows reading the FP32 gradient / a folded BF16 one: their table and BF16 destinations) and the
+        written addresses for a list of masters, checked row by row.  Later calls with the same masters and folded
+        rows reuse it; the operators check each call's tensors."""
+        rows = {False: [], True: []}
+        idx = {False: [], True: []}
+        written = []
+        for i, (g, p, m, v) in enumerate(zip(*tensor_lists)):
             n, d = self._row(g, p, m, v)
             if d is not None:
                 written.append(p.data_ptr())
-            rows.append((g, p, m, v, d, n))
-        table = self._tables.get(rows, rows[0][1].device)
-        plan = (table, ops.rows_lists(rows)[4], tuple(written))
-        self._plans[key] = plan
+            f = bool(folded and folded[i])
+            if f and (g16[i].dtype != torch.bfloat16 or not g16[i].is_contiguous() or g16[i].numel() != n):
+                raise RuntimeError('fused_adam_cast: a folded gradient must be contiguous bf16')
+            rows[f].append((g16[i] if f else g, p, m, v, d, n))
+            idx[f].append(i)
+        groups = []
+        for f in (False, True):
+            if rows[f]:
+                table = self._tables.get(rows[f], rows[f][0][1].device)
+                whole = len(idx[f]) == len(key)
+                groups.append((f, None if whole else tuple(idx[f]), table, ops.rows_lists(rows[f])[4]))
+        plan = (tuple(groups), tuple(written))
+        self._plans[(key, folded)] = plan
         while len(self._plans) > 8:
             self._plans.popitem(last=False)
         return plan
