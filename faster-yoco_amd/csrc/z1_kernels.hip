@@ -370,6 +370,54 @@ __device__ __forceinline__ void sumsq_chunk(const Row& r, int64_t c, int lane, d
     }
 }
 
+// The 128-bit group of chunk c a lane squares (false: the chunk takes sumsq_chunk's element-wise path).
+template <int GDT, bool KEEP>
+__device__ __forceinline__ bool sumsq_group(const Row& r, int64_t c, int lane, f4& x) {
+    const int64_t base = (c - r.chunk0) * kChunk;
+    if (r.n - base < kChunk || !(r.vec & kVecG)) return false;
+    const int64_t i = base + (int64_t)lane * kVec;
+    x = KEEP ? load_g4_keep<GDT>(r.g, i) : load_g4<GDT>(r.g, i);
+    return true;
+}
+
+// Chunks c, c + nw, c + 2 nw, ... below `end` into acc, in that order.  BF16 gradients give a wave 512 bytes per
+// chunk; one load in flight per wave reaches 4.4 TB/s on C2's size, so there kSumsqBf16Batch chunks' loads are
+// issued before any of them is added (4.7 TB/s).  The per-lane order of the additions, and with it every bit, stays
+// the fp32 kernel's (checked by comparing the partials of a bf16 table with those of its fp32 upcast).  FP32 keeps
+// one load in flight (more measured slower there).
+constexpr int kSumsqBf16Batch = 2;       // on C2's size 185.5-187.1 us, against 193.8-194.4 for 1, 189.9-190.2 for 4
+template <int GDT, bool KEEP>
+__device__ __forceinline__ void sumsq_range(const Row* __restrict__ rows, int nrows, int& t, int64_t& c, int64_t end,
+                                            int64_t nw, int lane, double& acc) {
+    if (GDT == Z1_BF16) {
+        constexpr int B = kSumsqBf16Batch;
+        for (; c + (B - 1) * nw < end; c += B * nw) {
+            int tr[B];
+            f4 x[B];
+            bool vx[B];
+#pragma unroll
+            for (int k = 0; k < B; ++k) {
+                t = advance_row(rows, nrows, t, c + k * nw);
+                tr[k] = t;
+                vx[k] = sumsq_group<GDT, KEEP>(rows[t], c + k * nw, lane, x[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < B; ++k) {
+                if (vx[k]) {
+#pragma unroll
+                    for (int e = 0; e < kVec; ++e) acc += sq64(x[k][e]);
+                } else {
+                    sumsq_chunk<GDT, KEEP>(rows[tr[k]], c + k * nw, lane, acc);
+                }
+            }
+        }
+    }
+    for (; c < end; c += nw) {
+        t = advance_row(rows, nrows, t, c);
+        sumsq_chunk<GDT, KEEP>(rows[t], c, lane, acc);
+    }
+}
+
 // Fixed grid of Z1_NORM_PARTIALS workgroups (a multiple of 8): the 256 workgroups b with b & 7 == x cover eighth x
 // of the chunks, wave w of them taking chunks lo_x + w, lo_x + w + 1024, ... (a workgroup covers 4 consecutive
 // chunks = 1024 contiguous elements per step); each lane adds its exact squares in that fixed order.
@@ -393,14 +441,8 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__
     double acc = 0.0;
     int t = 0;
     int64_t c = w0;
-    for (; c < split; c += nw) {
-        t = advance_row(rows, nrows, t, c);
-        sumsq_chunk<GDT, false>(rows[t], c, lane, acc);
-    }
-    for (; c < hi; c += nw) {
-        t = advance_row(rows, nrows, t, c);
-        sumsq_chunk<GDT, true>(rows[t], c, lane, acc);
-    }
+    sumsq_range<GDT, false>(rows, nrows, t, c, split, nw, lane, acc);
+    sumsq_range<GDT, true>(rows, nrows, t, c, hi, nw, lane, acc);
     const double s = block_sum(acc, lds);
     if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }

@@ -263,3 +263,27 @@ def test_adam_writes_the_scaled_gradients(pkg, dev, mode):
     with pytest.raises(RuntimeError, match='row 0 has 4999 elements'):
         ops.adam_cast(table, factor, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2, hp['weight_decay'],
                       mode, g32=[outs[0][1:]] + outs[1:])
+
+
+@pytest.mark.parametrize('total', [300_000, 150_000_000])
+def test_bf16_norm_partials_equal_the_fp32_kernels(pkg, dev, total):
+    """The norm pass over BF16 gradients (two chunks' loads in flight per wave) adds the same squares in the same
+    per-lane order as the FP32 pass: its Z1_NORM_PARTIALS partials equal, bit for bit, those of the FP32 pass over
+    the upcast values -- with rows off the vector alignment (element-wise chunks among the vector ones), short rows,
+    an empty row and, at 150M elements, the allocating loads of the MALL-kept part in both passes."""
+    from faster_yoco_amd import ops
+    gen = torch.Generator(device='cpu').manual_seed(total % 1000)
+    raw16 = (torch.randn(total + 64, generator=gen) * 1e-2).to(torch.bfloat16).to(dev)
+    raw32 = raw16.float()
+    cuts = [0, 1, 777, 5001, total // 3, total // 3 + 1, total // 3 + 1, total // 2 + 3, total]
+    rows16, rows32 = [], []
+    for a, b in zip(cuts, cuts[1:]):
+        rows16.append((raw16[a:b], None, None, None, None, b - a))
+        rows32.append((raw32[a:b], None, None, None, None, b - a))
+    p16, p32 = ops.norm_workspace(dev), ops.norm_workspace(dev)
+    ops.grad_sumsq(ops.Table(rows16, dev), p16)
+    ops.grad_sumsq(ops.Table(rows32, dev), p32)
+    torch.cuda.synchronize()
+    assert torch.equal(p16.view(torch.int64), p32.view(torch.int64))
+    exact = float(np.sqrt(oracle.sumsq(raw16[:total].view(torch.int16).cpu().numpy().view(np.uint16))))
+    assert abs(float(p16.sum().sqrt()) - exact) <= 1e-6 * exact
