@@ -370,57 +370,47 @@ __device__ __forceinline__ void sumsq_chunk(const Row& r, int64_t c, int lane, d
     }
 }
 
-// The 128-bit group of chunk c a lane squares (false: the chunk takes sumsq_chunk's element-wise path).
-template <int GDT, bool KEEP>
-__device__ __forceinline__ bool sumsq_group(const Row& r, int64_t c, int lane, f4& x) {
-    const int64_t base = (c - r.chunk0) * kChunk;
-    if (r.n - base < kChunk || !(r.vec & kVecG)) return false;
-    const int64_t i = base + (int64_t)lane * kVec;
-    x = KEEP ? load_g4_keep<GDT>(r.g, i) : load_g4<GDT>(r.g, i);
-    return true;
-}
-
-// Chunks c, c + nw, c + 2 nw, ... below `end` into acc, in that order.  BF16 gradients give a wave 512 bytes per
-// chunk; one load in flight per wave reaches 4.4 TB/s on C2's size, so there kSumsqBf16Batch chunks' loads are
-// issued before any of them is added (4.7 TB/s).  The per-lane order of the additions, and with it every bit, stays
-// the fp32 kernel's (checked by comparing the partials of a bf16 table with those of its fp32 upcast).  FP32 keeps
-// one load in flight (more measured slower there).
-constexpr int kSumsqBf16Batch = 2;       // on C2's size 185.5-187.1 us, against 193.8-194.4 for 1, 189.9-190.2 for 4
+// The chunks of one wave below `end` into acc, in order: for FP32, chunks c, c + step, c + 2 step, ... (one
+// 128-bit group per lane each); for BF16, chunk pairs (c, c + 1), (c + step, c + step + 1), ...: a pair inside one
+// row, whole and 16-byte aligned is one 128-bit load per lane (8 elements, the pair's lane-major order), other
+// pairs are their two chunks one after the other.  A BF16 chunk alone gives a wave 512 bytes per load, and the
+// per-chunk latency then bounds the pass: 188 us on C2's size (4.6 TB/s, even with two chunks' loads in flight)
+// against 141 us (6.1 TB/s) with the pairs.  Either way the order is fixed, so the partials are deterministic.
 template <int GDT, bool KEEP>
 __device__ __forceinline__ void sumsq_range(const Row* __restrict__ rows, int nrows, int& t, int64_t& c, int64_t end,
-                                            int64_t nw, int lane, double& acc) {
-    if (GDT == Z1_BF16) {
-        constexpr int B = kSumsqBf16Batch;
-        for (; c + (B - 1) * nw < end; c += B * nw) {
-            int tr[B];
-            f4 x[B];
-            bool vx[B];
-#pragma unroll
-            for (int k = 0; k < B; ++k) {
-                t = advance_row(rows, nrows, t, c + k * nw);
-                tr[k] = t;
-                vx[k] = sumsq_group<GDT, KEEP>(rows[t], c + k * nw, lane, x[k]);
-            }
-#pragma unroll
-            for (int k = 0; k < B; ++k) {
-                if (vx[k]) {
-#pragma unroll
-                    for (int e = 0; e < kVec; ++e) acc += sq64(x[k][e]);
-                } else {
-                    sumsq_chunk<GDT, KEEP>(rows[tr[k]], c + k * nw, lane, acc);
-                }
-            }
-        }
-    }
-    for (; c < end; c += nw) {
+                                            int64_t step, int lane, double& acc) {
+    for (; c < end; c += step) {
         t = advance_row(rows, nrows, t, c);
-        sumsq_chunk<GDT, KEEP>(rows[t], c, lane, acc);
+        const Row r = rows[t];
+        if (GDT == Z1_BF16) {
+            const uint16_t* g = static_cast<const uint16_t*>(r.g) + (c - r.chunk0) * kChunk;
+            const bool wide = c + 1 < end && r.n - (c - r.chunk0) * kChunk >= 2 * kChunk && (r.vec & kVecG) &&
+                              (reinterpret_cast<uintptr_t>(g) & 15) == 0;
+            if (wide) {
+                const u4* q = reinterpret_cast<const u4*>(g) + lane;
+                const u4 h = KEEP ? ld_keep(q) : ld(q);
+#pragma unroll
+                for (int w = 0; w < 4; ++w) {
+                    acc += sq64(bf16_lo(h[w]));
+                    acc += sq64(bf16_hi(h[w]));
+                }
+                continue;
+            }
+            sumsq_chunk<GDT, KEEP>(r, c, lane, acc);
+            if (c + 1 < end) {
+                t = advance_row(rows, nrows, t, c + 1);
+                sumsq_chunk<GDT, KEEP>(rows[t], c + 1, lane, acc);
+            }
+            continue;
+        }
+        sumsq_chunk<GDT, KEEP>(r, c, lane, acc);
     }
 }
 
 // Fixed grid of Z1_NORM_PARTIALS workgroups (a multiple of 8): the 256 workgroups b with b & 7 == x cover eighth x
 // of the chunks, wave w of them taking chunks lo_x + w, lo_x + w + 1024, ... (a workgroup covers 4 consecutive
-// chunks = 1024 contiguous elements per step); each lane adds its exact squares in that fixed order.
+// chunks = 1024 contiguous elements per step; for BF16, chunk pairs lo_x + 2w, lo_x + 2w + 2048, ...: 4 consecutive
+// pairs = 2048 elements per step); each lane adds its exact squares in that fixed order.
 // The last keep_per_eighth chunks of each eighth are read with ordinary loads (two loops, so that the two kinds of
 // load stay apart): they are where the Adam pass of each XCD starts (adam_cast_kernel walks every eighth from its
 // top), so every XCD's first gradient reads hit the MALL.
@@ -436,13 +426,15 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__
     const int64_t Q = nchunks >> 3, R = nchunks & 7;
     const int64_t lo = x * Q + (x < R ? x : R), hi = lo + Q + (x < R ? 1 : 0);
     const int64_t nw = (int64_t)(gridDim.x >> 3) * (kThreads / kWave);
-    const int64_t w0 = lo + j * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-    const int64_t split = hi - keep_per_eighth > lo ? hi - keep_per_eighth : lo;
+    const int64_t span = GDT == Z1_BF16 ? 2 : 1;      // chunks a wave takes per step
+    const int64_t w0 = lo + span * (j * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
+    int64_t split = hi - keep_per_eighth > lo ? hi - keep_per_eighth : lo;
+    split = lo + (split - lo + span - 1) / span * span;   // on the pair grid: no pair straddles the two loops
     double acc = 0.0;
     int t = 0;
     int64_t c = w0;
-    sumsq_range<GDT, false>(rows, nrows, t, c, split, nw, lane, acc);
-    sumsq_range<GDT, true>(rows, nrows, t, c, hi, nw, lane, acc);
+    sumsq_range<GDT, false>(rows, nrows, t, c, split < hi ? split : hi, span * nw, lane, acc);
+    sumsq_range<GDT, true>(rows, nrows, t, c, hi, span * nw, lane, acc);
     const double s = block_sum(acc, lds);
     if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }

@@ -266,11 +266,12 @@ def test_adam_writes_the_scaled_gradients(pkg, dev, mode):
 
 
 @pytest.mark.parametrize('total', [300_000, 150_000_000])
-def test_bf16_norm_partials_equal_the_fp32_kernels(pkg, dev, total):
-    """The norm pass over BF16 gradients (two chunks' loads in flight per wave) adds the same squares in the same
-    per-lane order as the FP32 pass: its Z1_NORM_PARTIALS partials equal, bit for bit, those of the FP32 pass over
-    the upcast values -- with rows off the vector alignment (element-wise chunks among the vector ones), short rows,
-    an empty row and, at 150M elements, the allocating loads of the MALL-kept part in both passes."""
+def test_bf16_norm_pass(pkg, dev, total):
+    """The norm pass over BF16 gradients (chunk pairs, one 128-bit load per lane where a pair is whole and aligned,
+    the two chunks one after the other elsewhere): rows off the vector alignment, short rows, an empty row and, at
+    150M elements, the allocating loads of the MALL-kept part.  Its partials are the same bits on every run, their
+    FP64 total is the FP32 pass's over the upcast values and the oracle's sequential sum to 1e-10 (sums of the same
+    exact squares in other orders), and the norm is within 1e-6 of the exact one."""
     from faster_yoco_amd import ops
     gen = torch.Generator(device='cpu').manual_seed(total % 1000)
     raw16 = (torch.randn(total + 64, generator=gen) * 1e-2).to(torch.bfloat16).to(dev)
@@ -280,10 +281,15 @@ def test_bf16_norm_partials_equal_the_fp32_kernels(pkg, dev, total):
     for a, b in zip(cuts, cuts[1:]):
         rows16.append((raw16[a:b], None, None, None, None, b - a))
         rows32.append((raw32[a:b], None, None, None, None, b - a))
-    p16, p32 = ops.norm_workspace(dev), ops.norm_workspace(dev)
-    ops.grad_sumsq(ops.Table(rows16, dev), p16)
+    t16 = ops.Table(rows16, dev)
+    p16, again, p32 = ops.norm_workspace(dev), ops.norm_workspace(dev), ops.norm_workspace(dev)
+    ops.grad_sumsq(t16, p16)
+    ops.grad_sumsq(t16, again)
     ops.grad_sumsq(ops.Table(rows32, dev), p32)
     torch.cuda.synchronize()
-    assert torch.equal(p16.view(torch.int64), p32.view(torch.int64))
-    exact = float(np.sqrt(oracle.sumsq(raw16[:total].view(torch.int16).cpu().numpy().view(np.uint16))))
-    assert abs(float(p16.sum().sqrt()) - exact) <= 1e-6 * exact
+    assert torch.equal(p16.view(torch.int64), again.view(torch.int64))
+    s16, s32 = float(p16.sum()), float(p32.sum())
+    seq = oracle.sumsq(raw16[:total].view(torch.int16).cpu().numpy().view(np.uint16))
+    assert abs(s16 - s32) <= 1e-10 * s32 and abs(s16 - seq) <= 1e-10 * seq
+    exact = float(np.sqrt(seq))
+    assert abs(float(np.sqrt(s16)) - exact) <= 1e-6 * exact

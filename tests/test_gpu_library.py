@@ -88,6 +88,9 @@ def test_opcheck_operators(pkg, dev):
         (Y.clip_factor_.default, (torch.tensor([3.0], device=dev), one(), one(), 1.0, 0.5)),
         (Y.adam_cast_.default, (table.handle_int, [g], [p], [m], [v], [p16], None, 3e-4, 0.9, 0.95, 1e-8, 0.1,
                                 0.05, 0.1, 1, 0, 1)),
+        (Y.adam_cast_gout_.default, (table.handle_int, [g], [p], [m], [v], [p16], [torch.empty(n, device=dev)],
+                                     torch.tensor([0.5], device=dev), 3e-4, 0.9, 0.95, 1e-8, 0.1, 0.05, 0.1, 1, 0,
+                                     1)),
         (Y.owner_sum_.default, ([p16, p16.clone()], torch.empty(n, dtype=torch.bfloat16, device=dev), 0.5, None,
                                 ops.norm_workspace(dev, n))),
         (Y.scale_up_.default, (p16, torch.empty(n, device=dev), torch.tensor([0.25], device=dev))),
