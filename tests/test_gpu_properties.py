@@ -1,6 +1,6 @@
 """Property-based GPU parity (hypothesis): random tensor tables -- row counts, ragged sizes (including 0 and tails),
-per-array misalignment, bf16 or fp32 gradients, with or without BF16 copies, both Adam modes, random factors and
-steps -- random owner sums (world 1..16, odd lengths, offsets), norms of random tables with the clip chain, the
+per-array misalignment, bf16 or fp32 gradients, with or without BF16 copies and FP32 gradient outputs, both Adam
+modes, random factors and steps -- random owner sums (world 1..16, odd lengths, offsets), norms of random tables with the clip chain, the
 embedding gradient over random ids, widths, padding and scale placements, and the scale / cast passes at random
 sizes and offsets; each checked against the oracle (bit-exact; the norm within 1e-6 of the exact value)."""
 import numpy as np
@@ -32,14 +32,17 @@ def place(arr, off, dev, bf16=False):
        offs=st.lists(st.integers(0, 7), min_size=5, max_size=5),
        g_bf16=st.booleans(), with_p16=st.booleans(), mode=st.sampled_from([0, 1]),
        factor=st.one_of(st.none(), st.floats(1e-8, 4.0)), step=st.integers(1, 3000),
-       cuts=st.lists(st.integers(0, 8), max_size=4), seed=st.integers(0, 2 ** 31 - 1))
-def test_adam_random_tables(pkg, dev, sizes, offs, g_bf16, with_p16, mode, factor, step, cuts, seed):
+       cuts=st.lists(st.integers(0, 8), max_size=4), with_gout=st.booleans(), goff=st.integers(0, 7),
+       seed=st.integers(0, 2 ** 31 - 1))
+def test_adam_random_tables(pkg, dev, sizes, offs, g_bf16, with_p16, mode, factor, step, cuts, with_gout, goff,
+                            seed):
     """Adam + BF16 over a random table against the oracle; with `cuts`, as one z1_adam_cast_rows launch per range
-    between the cut rows."""
+    between the cut rows; with FP32 gradient outputs (at a random misalignment), each holding the oracle's scaled
+    gradient afterwards."""
     from faster_yoco_amd import ops
     rng = np.random.default_rng(seed)
     hp = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
-    rows, keep, ref = [], [], []
+    rows, keep, ref, outs, want = [], [], [], [], []
     for n in sizes:
         g = (rng.standard_normal(n) * 10.0 ** rng.uniform(-5, 0)).astype(np.float32)
         g = oracle.bf16_rne(g) if g_bf16 else g
@@ -52,6 +55,9 @@ def test_adam_random_tables(pkg, dev, sizes, offs, g_bf16, with_p16, mode, facto
         rows.append((gt, pt, mt, vt, p16, n))
         keep.append((pt, mt, vt, p16))
         ref.append(oracle.adam_cast(g, p, m, v, step=step, mode=mode, factor=factor, **hp))
+        outs.append(place(np.full(n, -7.0, np.float32), goff, dev))
+        f1 = np.float32(1.0 if factor is None else factor)
+        want.append(oracle.scale_up(g, f1) if g_bf16 else (g * f1).astype(np.float32))
     table = ops.Table(rows, dev)
     bc1, bc2 = ops.bias_corrections(hp['beta1'], hp['beta2'], step)
     f = None if factor is None else torch.tensor([factor], dtype=torch.float32, device=dev)
@@ -59,10 +65,15 @@ def test_adam_random_tables(pkg, dev, sizes, offs, g_bf16, with_p16, mode, facto
         bounds = sorted({0, len(sizes)} | {c for c in cuts if c <= len(sizes)})
         for a, b in zip(bounds, bounds[1:]):
             ops.adam_cast_rows(table, a, b, f, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2,
-                               hp['weight_decay'], mode)
+                               hp['weight_decay'], mode, g32=outs if with_gout else None)
     else:
-        ops.adam_cast(table, f, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2, hp['weight_decay'], mode)
+        ops.adam_cast(table, f, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2, hp['weight_decay'], mode,
+                      g32=outs if with_gout else None)
     torch.cuda.synchronize()
+    for o, w in zip(outs, want):
+        got = o.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), w.view(np.uint32) if with_gout else np.full_like(got, -7.0).view(
+            np.uint32))
     for (pt, mt, vt, p16), (po, mo, vo, p16o) in zip(keep, ref):
         assert np.array_equal(pt.cpu().numpy().view(np.uint32), po.view(np.uint32))
         assert np.array_equal(mt.cpu().numpy().view(np.uint32), mo.view(np.uint32))
