@@ -370,12 +370,14 @@ __device__ __forceinline__ void sumsq_chunk(const Row& r, int64_t c, int lane, d
     }
 }
 
-// The chunks of one wave below `end` into acc, in order: for FP32, chunks c, c + step, c + 2 step, ... (one
-// 128-bit group per lane each); for BF16, chunk pairs (c, c + 1), (c + step, c + step + 1), ...: a pair inside one
-// row, whole and 16-byte aligned is one 128-bit load per lane (8 elements, the pair's lane-major order), other
-// pairs are their two chunks one after the other.  A BF16 chunk alone gives a wave 512 bytes per load, and the
-// per-chunk latency then bounds the pass: 188 us on C2's size (4.6 TB/s, even with two chunks' loads in flight)
-// against 141 us (6.1 TB/s) with the pairs.  Either way the order is fixed, so the partials are deterministic.
+// The chunks of one wave below `end` into acc, in order.  FP32: chunks c, c + step, c + 2 step, ... (one 128-bit
+// group per lane each).  BF16: runs of kSumsqBf16Span adjacent chunks starting at c, c + step, ...: a run inside one
+// row, whole and 16-byte aligned, is kSumsqBf16Span / 2 128-bit loads per lane (8 elements each: the run's
+// lane-major order, one 1 KB load of the wave after the other); other runs are their chunks one after the other.
+// A BF16 chunk alone gives a wave 512 bytes per load, and the per-chunk latency then bounds the pass (188 us on
+// C2's size, 4.6 TB/s, even with two chunks' loads in flight); runs of 2, 4, 8 and 16 chunks measured 143, 135,
+// 136 and 143 us.  Either way the order is fixed, so the partials are deterministic.
+constexpr int kSumsqBf16Span = 4;
 template <int GDT, bool KEEP>
 __device__ __forceinline__ void sumsq_range(const Row* __restrict__ rows, int nrows, int& t, int64_t& c, int64_t end,
                                             int64_t step, int lane, double& acc) {
@@ -383,23 +385,29 @@ __device__ __forceinline__ void sumsq_range(const Row* __restrict__ rows, int nr
         t = advance_row(rows, nrows, t, c);
         const Row r = rows[t];
         if (GDT == Z1_BF16) {
+            constexpr int S = kSumsqBf16Span, L = kSumsqBf16Span / 2;
             const uint16_t* g = static_cast<const uint16_t*>(r.g) + (c - r.chunk0) * kChunk;
-            const bool wide = c + 1 < end && r.n - (c - r.chunk0) * kChunk >= 2 * kChunk && (r.vec & kVecG) &&
+            const bool wide = c + (S - 1) < end && r.n - (c - r.chunk0) * kChunk >= S * kChunk && (r.vec & kVecG) &&
                               (reinterpret_cast<uintptr_t>(g) & 15) == 0;
             if (wide) {
                 const u4* q = reinterpret_cast<const u4*>(g) + lane;
-                const u4 h = KEEP ? ld_keep(q) : ld(q);
+                u4 h[L];
 #pragma unroll
-                for (int w = 0; w < 4; ++w) {
-                    acc += sq64(bf16_lo(h[w]));
-                    acc += sq64(bf16_hi(h[w]));
+                for (int u = 0; u < L; ++u) h[u] = KEEP ? ld_keep(q + u * kWave) : ld(q + u * kWave);
+#pragma unroll
+                for (int u = 0; u < L; ++u) {
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) {
+                        acc += sq64(bf16_lo(h[u][w]));
+                        acc += sq64(bf16_hi(h[u][w]));
+                    }
                 }
                 continue;
             }
             sumsq_chunk<GDT, KEEP>(r, c, lane, acc);
-            if (c + 1 < end) {
-                t = advance_row(rows, nrows, t, c + 1);
-                sumsq_chunk<GDT, KEEP>(rows[t], c + 1, lane, acc);
+            for (int64_t e = c + 1; e < c + S && e < end; ++e) {
+                t = advance_row(rows, nrows, t, e);
+                sumsq_chunk<GDT, KEEP>(rows[t], e, lane, acc);
             }
             continue;
         }
@@ -409,8 +417,9 @@ __device__ __forceinline__ void sumsq_range(const Row* __restrict__ rows, int nr
 
 // Fixed grid of Z1_NORM_PARTIALS workgroups (a multiple of 8): the 256 workgroups b with b & 7 == x cover eighth x
 // of the chunks, wave w of them taking chunks lo_x + w, lo_x + w + 1024, ... (a workgroup covers 4 consecutive
-// chunks = 1024 contiguous elements per step; for BF16, chunk pairs lo_x + 2w, lo_x + 2w + 2048, ...: 4 consecutive
-// pairs = 2048 elements per step); each lane adds its exact squares in that fixed order.
+// chunks = 1024 contiguous elements per step; for BF16, runs of kSumsqBf16Span chunks starting at lo_x + 4w,
+// lo_x + 4w + 4096, ...: 4 consecutive runs = 4096 elements per step); each lane adds its exact squares in that
+// fixed order.
 // The last keep_per_eighth chunks of each eighth are read with ordinary loads (two loops, so that the two kinds of
 // load stay apart): they are where the Adam pass of each XCD starts (adam_cast_kernel walks every eighth from its
 // top), so every XCD's first gradient reads hit the MALL.
@@ -426,10 +435,10 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__
     const int64_t Q = nchunks >> 3, R = nchunks & 7;
     const int64_t lo = x * Q + (x < R ? x : R), hi = lo + Q + (x < R ? 1 : 0);
     const int64_t nw = (int64_t)(gridDim.x >> 3) * (kThreads / kWave);
-    const int64_t span = GDT == Z1_BF16 ? 2 : 1;      // chunks a wave takes per step
+    const int64_t span = GDT == Z1_BF16 ? kSumsqBf16Span : 1;   // chunks a wave takes per step
     const int64_t w0 = lo + span * (j * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
     int64_t split = hi - keep_per_eighth > lo ? hi - keep_per_eighth : lo;
-    split = lo + (split - lo + span - 1) / span * span;   // on the pair grid: no pair straddles the two loops
+    split = lo + (split - lo + span - 1) / span * span;   // on the run grid: no run straddles the two loops
     double acc = 0.0;
     int t = 0;
     int64_t c = w0;
