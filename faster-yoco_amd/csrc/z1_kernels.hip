@@ -57,7 +57,7 @@ namespace {
 
 // Launch geometry (the measured choices on MI355X; alternatives and their timings are recorded with the design):
 constexpr int kWave = 64;
-constexpr int kThreads = 256;                                 // norm / owner-sum / scale / cast workgroups
+constexpr int kThreads = 256;                                 // norm and one-workgroup reduction workgroups
 constexpr int kAdamWaves = 1;                                 // chunks (one per wave) per Adam workgroup
 constexpr int kVec = 4;                                       // fp32 lanes of one 128-bit access
 constexpr int kGroups = 1;                                    // 128-bit groups per lane per array and chunk
@@ -630,49 +630,53 @@ __global__ __launch_bounds__(kRebindPerLaunch) void rebind_rows_kernel(Row* rows
 }
 
 // ------------------------------------------------------------------------------------- scale / cast passes
-__global__ __launch_bounds__(kThreads) void scale_up_kernel(const uint16_t* __restrict__ g16, float* __restrict__ g32,
-                                                            const float* __restrict__ factor, int64_t n, int vec) {
+// The scale and cast passes: one wave per kPassChunk-element chunk, dispatched by the hardware with the
+// XCD-contiguous map, every load and store instruction of a wave covering one contiguous span (two 4-element
+// groups per lane, kPassChunk / 2 elements apart).  A grid-stride loop over the whole array, one 16-byte load in
+// flight per wave, reached 3.9 TB/s (scale) and 5.4 TB/s (cast) on 430M elements.
+constexpr int64_t kPassChunk = (int64_t)kWave * 8;
+
+__global__ __launch_bounds__(kWave) void scale_up_kernel(const uint16_t* __restrict__ g16, float* __restrict__ g32,
+                                                         const float* __restrict__ factor, int64_t n, int vec) {
+    const int64_t e0 = chunk_of_block(blockIdx.x, gridDim.x) * kPassChunk;
     const float f = *factor;
-    const int64_t nthreads = (int64_t)gridDim.x * kThreads;
-    const int64_t gtid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    int64_t tail0 = 0;
-    if (vec) {
-        const int64_t ng = n / 8;
-        tail0 = ng * 8;
-        for (int64_t gi = gtid; gi < ng; gi += nthreads) {
-            const u4 h = ld(reinterpret_cast<const u4*>(g16) + gi);
-            st(reinterpret_cast<f4*>(g32) + 2 * gi, f4{bf16_lo(h.x) * f, bf16_hi(h.x) * f, bf16_lo(h.y) * f,
-                                                        bf16_hi(h.y) * f});
-            st(reinterpret_cast<f4*>(g32) + 2 * gi + 1, f4{bf16_lo(h.z) * f, bf16_hi(h.z) * f, bf16_lo(h.w) * f,
-                                                            bf16_hi(h.w) * f});
-        }
+    const int lane = threadIdx.x;
+    if (vec && e0 + kPassChunk <= n) {
+        u2 h[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) h[u] = ld(reinterpret_cast<const u2*>(g16 + e0 + u * (kPassChunk / 2)) + lane);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            st(reinterpret_cast<f4*>(g32 + e0 + u * (kPassChunk / 2)) + lane,
+               f4{bf16_lo(h[u].x) * f, bf16_hi(h[u].x) * f, bf16_lo(h[u].y) * f, bf16_hi(h[u].y) * f});
+        return;
     }
-    for (int64_t e = tail0 + gtid; e < n; e += nthreads) g32[e] = bf16_to_f32(g16[e]) * f;
+    const int64_t e1 = e0 + kPassChunk < n ? e0 + kPassChunk : n;
+    for (int64_t e = e0 + lane; e < e1; e += kWave) g32[e] = bf16_to_f32(g16[e]) * f;
 }
 
-__global__ __launch_bounds__(kThreads) void cast_bf16_kernel(const float* __restrict__ p32, uint16_t* __restrict__ p16,
-                                                             int64_t n, int vec) {
-    const int64_t nthreads = (int64_t)gridDim.x * kThreads;
-    const int64_t gtid = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-    int64_t tail0 = 0;
-    if (vec) {
-        const int64_t ng = n / 8;
-        tail0 = ng * 8;
-        for (int64_t gi = gtid; gi < ng; gi += nthreads) {
-            const f4 a = ld(reinterpret_cast<const f4*>(p32) + 2 * gi);
-            const f4 b = ld(reinterpret_cast<const f4*>(p32) + 2 * gi + 1);
-            st(reinterpret_cast<u4*>(p16) + gi,
-               u4{pack_bf16(a.x, a.y), pack_bf16(a.z, a.w), pack_bf16(b.x, b.y), pack_bf16(b.z, b.w)});
-        }
+__global__ __launch_bounds__(kWave) void cast_bf16_kernel(const float* __restrict__ p32, uint16_t* __restrict__ p16,
+                                                          int64_t n, int vec) {
+    const int64_t e0 = chunk_of_block(blockIdx.x, gridDim.x) * kPassChunk;
+    const int lane = threadIdx.x;
+    if (vec && e0 + kPassChunk <= n) {
+        f4 a[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) a[u] = ld(reinterpret_cast<const f4*>(p32 + e0 + u * (kPassChunk / 2)) + lane);
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+            st(reinterpret_cast<u2*>(p16 + e0 + u * (kPassChunk / 2)) + lane,
+               u2{pack_bf16(a[u].x, a[u].y), pack_bf16(a[u].z, a[u].w)});
+        return;
     }
-    for (int64_t e = tail0 + gtid; e < n; e += nthreads) p16[e] = (uint16_t)f32_to_bf16(p32[e]);
+    const int64_t e1 = e0 + kPassChunk < n ? e0 + kPassChunk : n;
+    for (int64_t e = e0 + lane; e < e1; e += kWave) p16[e] = (uint16_t)f32_to_bf16(p32[e]);
 }
 
 // -------------------------------------------------------------------------------------------- host helpers
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
 struct DevInfo {
-    int cus = 0;
     int lds_per_cu = -1;       // bytes of LDS per CU; -1: not read yet
 };
 
@@ -683,18 +687,6 @@ int current_device(int* dev) {
     hipError_t e = hipGetDevice(dev);
     if (e != hipSuccess) return (int)e;
     if (*dev < 0 || *dev >= kMaxDevices) return Z1_E_DEVICE;
-    return Z1_OK;
-}
-
-int cu_count(int dev, int* cus) {
-    std::lock_guard<std::mutex> lk(g_mu);
-    if (g_dev[dev].cus == 0) {
-        int v = 0;
-        hipError_t e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev);
-        if (e != hipSuccess) return (int)e;
-        g_dev[dev].cus = v > 0 ? v : 1;
-    }
-    *cus = g_dev[dev].cus;
     return Z1_OK;
 }
 
@@ -714,17 +706,6 @@ int occupancy_lds(int dev, int per_cu, size_t* bytes) {
     size_t b = (size_t)g_dev[dev].lds_per_cu / (size_t)per_cu;
     b &= ~(size_t)511;
     *bytes = b > 65536 ? 65536 : b;
-    return Z1_OK;
-}
-
-int stream_grid(int dev, int64_t groups, int* grid) {
-    int cus = 0;
-    int rc = cu_count(dev, &cus);
-    if (rc) return rc;
-    int64_t want = (groups + kThreads - 1) / kThreads;
-    int64_t cap = (int64_t)cus * 8;
-    if (want > cap) want = cap;
-    *grid = (int)(want < 1 ? 1 : want);
     return Z1_OK;
 }
 
@@ -1243,14 +1224,11 @@ int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n,
     if (n < 0) return Z1_E_SIZE;
     if (n == 0) return Z1_OK;
     if (!g16 || !g32 || !factor) return Z1_E_NULL;
-    int dev = 0, grid = 0;
-    int rc = current_device(&dev);
-    if (rc) return rc;
-    rc = stream_grid(dev, n / 8 + (n % 8 != 0), &grid);
-    if (rc) return rc;
-    const int vec = aligned(g16, 16) && aligned(g32, 16);
-    hipLaunchKernelGGL(scale_up_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), g16, g32,
-                       factor, n, vec);
+    const int64_t chunks = (n + kPassChunk - 1) / kPassChunk;
+    if (chunks > INT32_MAX) return Z1_E_SIZE;
+    const int vec = aligned(g16, 8) && aligned(g32, 16);
+    hipLaunchKernelGGL(scale_up_kernel, dim3((unsigned)chunks), dim3(kWave), 0, static_cast<hipStream_t>(stream),
+                       g16, g32, factor, n, vec);
     return launch_status();
 }
 
@@ -1258,14 +1236,11 @@ int z1_cast_bf16(const float* p32, uint16_t* p16, int64_t n, void* stream) {
     if (n < 0) return Z1_E_SIZE;
     if (n == 0) return Z1_OK;
     if (!p32 || !p16) return Z1_E_NULL;
-    int dev = 0, grid = 0;
-    int rc = current_device(&dev);
-    if (rc) return rc;
-    rc = stream_grid(dev, n / 8 + (n % 8 != 0), &grid);
-    if (rc) return rc;
-    const int vec = aligned(p32, 16) && aligned(p16, 16);
-    hipLaunchKernelGGL(cast_bf16_kernel, dim3(grid), dim3(kThreads), 0, static_cast<hipStream_t>(stream), p32, p16, n,
-                       vec);
+    const int64_t chunks = (n + kPassChunk - 1) / kPassChunk;
+    if (chunks > INT32_MAX) return Z1_E_SIZE;
+    const int vec = aligned(p32, 16) && aligned(p16, 8);
+    hipLaunchKernelGGL(cast_bf16_kernel, dim3((unsigned)chunks), dim3(kWave), 0, static_cast<hipStream_t>(stream),
+                       p32, p16, n, vec);
     return launch_status();
 }
 
