@@ -1,6 +1,8 @@
 """The shard update captured in a HIP graph (torch.cuda.graph): norm + clip + Adam + BF16 copy, and the owner-sum
 form (owner sum with the fused norm, clip, Adam), each replayed several times from a restored state -- with eager
 work and synchronisations between the replays -- and every replay bit-identical to the same update run eagerly.
+Likewise the owner's embedding gradient, and the drop-in's FusedAdamCast call (folded BF16 gradients, FP32
+gradients written) after one eager call.
 
 The update launches only kernels on the current stream (the tables and the norm workspace are made at set-up, and
 nothing in it clears memory with a memset), so it can be captured once per step and replayed; the bias corrections
@@ -189,3 +191,51 @@ def test_owner_embedding_grad_graph_replays_match_eager(pkg, dev, R, zipf):
         torch.cuda.synchronize()
         assert torch.equal(got.view(torch.int16), eager.view(torch.int16))
         assert torch.equal(got.view(torch.int16), aten.view(torch.int16))
+
+
+def test_dropin_fused_adam_graph_replays_match_eager(pkg, dev):
+    """The drop-in's default Adam call -- FusedAdamCast over per-parameter tensors with the BF16 gradients folded in
+    and the FP32 gradients written by the same launch -- captured after one eager call (which makes the tables and
+    the plan) and replayed three times from a restored state: every replay equals the eager call bit for bit,
+    masters, moments, BF16 copies and the written FP32 gradients."""
+    from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+    shapes = [(96, 64), (3, 1000), (4096,), (7,), (256, 33)]
+    gen = torch.Generator(device='cpu').manual_seed(17)
+    mk = lambda s, sd: (torch.randn(*s, generator=gen) * sd).to(dev)
+    p = [mk(s, 0.02) for s in shapes]
+    m = [mk(s, 1e-4) for s in shapes]
+    v = [mk(s, 1e-8).abs() for s in shapes]
+    g32 = [torch.zeros(s, device=dev) for s in shapes]
+    g16 = [mk(s, 1e-2).to(torch.bfloat16) for s in shapes]
+    p16 = [torch.zeros(s, dtype=torch.bfloat16, device=dev) for s in shapes]
+    fa = FusedAdamCast({a.data_ptr(): b for a, b in zip(p, p16)})
+    fa.fold, fa.fold_factor, fa.fold_writes = {a.data_ptr(): b for a, b in zip(p, g16)}, \
+        torch.tensor([0.37], device=dev), True
+    state = [p, m, v, g32, p16]
+    start = [[t.clone() for t in X] for X in state]
+
+    def call():
+        fa(2048 * 32, None, [g32, p, m, v], 3e-4, 0.9, 0.95, 1e-8, 5, 1, 1, 0.1)
+
+    def restore_state():
+        for X, S in zip(state, start):
+            for t, s in zip(X, S):
+                t.copy_(s)
+    call()                                            # eager: tables, plan, and the reference result
+    torch.cuda.synchronize()
+    eager = [[t.clone() for t in X] for X in state]
+    restore_state()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for _ in range(3):
+        restore_state()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for X, E in zip(state, eager):
+            for t, e in zip(X, E):
+                assert torch.equal(t.view(torch.int16) if t.dtype == torch.bfloat16 else t.view(torch.int32),
+                                   e.view(torch.int16) if e.dtype == torch.bfloat16 else e.view(torch.int32))
+    assert fa.cast == {a.data_ptr() for a in p}
