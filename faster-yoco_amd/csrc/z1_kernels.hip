@@ -5,12 +5,13 @@
 //     kChunk = 256 elements (one wave64 x one float4 per lane); row r owns the global chunk range
 //     [chunk0_r, chunk0_r + ceil(n_r / kChunk)).  A chunk -> row map (one int32 per chunk) follows the rows in
 //     the same device allocation, so a wave finds its row with two scalar loads.
-//   * Adam + BF16: one wave per chunk, one wave per workgroup, dispatched by the hardware (grid = chunks).  The
-//     workgroup -> chunk map undoes the round-robin dispatch over the 8 XCDs, so each XCD streams one contiguous
-//     eighth of the shard, taken from its last chunk down (see the MALL note below); a dynamic LDS reservation
-//     the kernel does not touch caps it at 16 resident workgroups per CU.  Measured on MI355X (431M-element
-//     shard): 2.05 ms on typical boxes, against 2.52 ms for a persistent grid with a static partition (tail
-//     imbalance across CUs/XCDs) and 2.19 ms for 1024-element workgroups; the same kernel with its arithmetic
+//   * Adam + BF16: one wave per chunk, one wave per workgroup, dispatched by the hardware (grid = chunks).
+//     Workgroup b takes the b-th chunk from the end, so the hardware's round-robin dispatch over the 8 XCDs
+//     interleaves consecutive chunks over all XCDs, and all of them start on the MALL-resident end of the shard
+//     (see the MALL note below); a dynamic LDS reservation the kernel does not touch caps it at 16 resident
+//     workgroups per CU.  Measured on MI355X (431M-element shard): 2.02-2.03 ms, against 2.05 ms when each XCD
+//     streams one contiguous eighth, 2.52 ms for a persistent grid with a static partition (tail imbalance
+//     across CUs/XCDs) and 2.19 ms for 1024-element workgroups; the same kernel with its arithmetic
 //     replaced by additions runs at the same speed, i.e. it is at the bandwidth this 4-read / 4-write stream
 //     pattern reaches.  A launch covers a chunk range: the whole table, or the chunks of a range of rows
 //     (z1_adam_cast_rows), so a step can be cut into launches whose finished rows are sent while the rest runs
@@ -27,10 +28,9 @@
 //     wave per chunk with hardware dispatch (0.40 ms), 4-chunk workgroups with hardware dispatch (0.34 ms),
 //     2-8 loads in flight per wave (0.28-0.31 ms) and fewer waves (0.35-0.59 ms) were all slower.
 //   * MALL reuse between passes: the pass before Adam (the norm, or the owner sum that writes the BF16 average)
-//     touches 256 (224) MB of the gradient with ordinary, allocating accesses where Adam starts, and Adam walks
-//     the chunks from the last one, so its first gradient reads hit the 256 MB MALL (measured 2.05 vs 2.10 ms for
-//     Adam on the C2 shard; 128-512 MB kept, or everything, measured the same or slower).  The norm keeps the top
-//     of each XCD's eighth, where that XCD's Adam workgroups start.
+//     touches the last 256 (224) MB of the gradient with ordinary, allocating accesses, and Adam walks the
+//     chunks from the last one, so its first gradient reads hit the 256 MB MALL (measured 2.05 vs 2.10 ms for
+//     Adam on the C2 shard; 128-512 MB kept, or everything, measured the same or slower).
 //   * No atomics anywhere; nothing but vector memory instructions write memory.  (The norm's final reduction is a
 //     second, one-workgroup launch: folding it into the last workgroup of the norm grid to finish, with an arrival
 //     counter, measured 75 us slower per step, because the grid's 2048 workgroups finish together.)
@@ -123,7 +123,9 @@ __device__ __forceinline__ void st_keep(T* p, T x) {     // ordinary store: allo
 }
 
 // Chunk of workgroup b: undoes the round-robin dispatch over the 8 XCDs (workgroup b runs on XCD b mod 8), so that
-// each XCD streams one contiguous eighth of the chunks (measured 2.10 vs 2.14 ms for the plain b -> b map).
+// each XCD streams one contiguous eighth of the chunks.  Used by the scale and cast passes; Adam and the owner sum
+// measured faster with the plain b -> b map (consecutive chunks interleaved over the XCDs: C2 update 2.283 vs
+// 2.306 ms, C3 3.153 vs 3.225 ms, interleaved A/B runs on one box).
 __device__ __forceinline__ int64_t chunk_of_block(int64_t b, int64_t nb) {
     const int64_t x = b & 7, q = b >> 3, Q = nb >> 3, R = nb & 7;
     return x * Q + (x < R ? x : R) + q;
@@ -196,9 +198,9 @@ __global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row
                                                                        const float* __restrict__ bc, AdamK k,
                                                                        float* const* __restrict__ gout) {
     const int lane = threadIdx.x & (kWave - 1);
-    // chunks [chunk_begin, chunk_end), last chunk first: the end of the gradient is what the norm pass read last
-    // (still in the MALL)
-    const int64_t c = chunk_end - 1 - (chunk_of_block(blockIdx.x, gridDim.x) * kAdamWaves +
+    // chunks [chunk_begin, chunk_end), last chunk first: the end of the gradient is what the pass before left in
+    // the MALL.  Consecutive workgroups take consecutive chunks and land on consecutive XCDs.
+    const int64_t c = chunk_end - 1 - ((int64_t)blockIdx.x * kAdamWaves +
                                        __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
     if (c < chunk_begin) return;
     const float f = factor ? *factor : 1.0f;
@@ -420,12 +422,12 @@ __device__ __forceinline__ void sumsq_range(const Row* __restrict__ rows, int nr
 // chunks = 1024 contiguous elements per step; for BF16, runs of kSumsqBf16Span chunks starting at lo_x + 4w,
 // lo_x + 4w + 4096, ...: 4 consecutive runs = 4096 elements per step); each lane adds its exact squares in that
 // fixed order.
-// The last keep_per_eighth chunks of each eighth are read with ordinary loads (two loops, so that the two kinds of
-// load stay apart): they are where the Adam pass of each XCD starts (adam_cast_kernel walks every eighth from its
-// top), so every XCD's first gradient reads hit the MALL.
+// Chunks [keep_from, nchunks) are read with ordinary loads (two loops, so that the two kinds of load stay apart):
+// they are where the Adam pass starts (adam_cast_kernel walks the chunks from the last one down), so its first
+// gradient reads hit the MALL.
 template <int GDT>
 __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__ rows, int nrows, int64_t nchunks,
-                                                         int64_t keep_per_eighth, double* __restrict__ partials) {
+                                                         int64_t keep_from, double* __restrict__ partials) {
     __shared__ double lds[kThreads / kWave];
     const int lane = threadIdx.x & (kWave - 1);
     // workgroup b strides through eighth (b & 7) of the chunks only: the eighth the XCD it is dispatched to
@@ -437,7 +439,7 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__
     const int64_t nw = (int64_t)(gridDim.x >> 3) * (kThreads / kWave);
     const int64_t span = GDT == Z1_BF16 ? kSumsqBf16Span : 1;   // chunks a wave takes per step
     const int64_t w0 = lo + span * (j * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
-    int64_t split = hi - keep_per_eighth > lo ? hi - keep_per_eighth : lo;
+    int64_t split = keep_from > lo ? (keep_from < hi ? keep_from : hi) : lo;
     split = lo + (split - lo + span - 1) / span * span;   // on the run grid: no run straddles the two loops
     double acc = 0.0;
     int t = 0;
@@ -473,20 +475,21 @@ struct Srcs {
     const uint16_t* p[Z1_MAX_WORLD];
 };
 
-// Owner sum: one wave per chunk of kSumChunk = 512 elements (8 per lane, 16 B per contribution), dispatched by
-// the hardware with the XCD-contiguous map (measured 6.0 TB/s for this 8-read / 1-write pattern against 4.5 TB/s
-// for a static grid-stride partition).  W is a compile-time constant so that all W loads of a lane are in flight
-// together (a runtime count makes the compiler wait on each load before issuing the next).  OUT may alias one
-// source: every element is read before the same lane writes it.  With wave_partials, lane 0 of each wave writes
-// the FP64 sum of squares of its chunk's rounded averages to wave_partials[chunk] (a fixed decomposition; the
-// partials are then reduced in a fixed order by reduce_partials_kernel).
+// Owner sum: one wave per chunk of kSumChunk = 512 elements (8 per lane, 16 B per contribution), workgroup b on
+// chunk b, dispatched by the hardware round-robin over the XCDs (measured 6.2 TB/s for this 8-read / 1-write
+// pattern, against 6.0 TB/s with each XCD on one contiguous eighth and 4.5 TB/s for a static grid-stride
+// partition).  W is a compile-time constant so that all W loads of a lane are in flight together (a runtime count
+// makes the compiler wait on each load before issuing the next).  OUT may alias one source: every element is read
+// before the same lane writes it.  With wave_partials, lane 0 of each wave writes the FP64 sum of squares of its
+// chunk's rounded averages to wave_partials[chunk] (a fixed decomposition; the partials are then reduced in a
+// fixed order by reduce_partials_kernel).
 constexpr int64_t kSumChunk = (int64_t)kWave * 8;
 
 template <int W, bool KEEP>
 __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, float scale, uint16_t* out,
                                                           float* out_sum, double* wave_partials, int vec,
                                                           int64_t chunk_base) {
-    const int64_t c = chunk_base + chunk_of_block(blockIdx.x, gridDim.x);
+    const int64_t c = chunk_base + (int64_t)blockIdx.x;
     const int64_t e0 = c * kSumChunk + (int64_t)threadIdx.x * 8;
     double acc2 = 0.0;
     if (vec && e0 + 8 <= n) {
@@ -988,11 +991,11 @@ int z1_table_set_grad_out(z1_table* table, float* const* g32, int nrows, void* s
     return Z1_OK;
 }
 
-// Chunks of each eighth of a table that the norm reads with allocating loads (kMallKeepBytes of gradient over the 8
-// eighths, see sumsq_kernel).
-static int64_t keep_per_eighth(const z1_table* table) {
+// First chunk of a table that the norm reads with allocating loads: the last kMallKeepBytes of gradient.
+static int64_t keep_from(const z1_table* table) {
     const int64_t chunk_bytes = kChunk * (table->g_dtype == Z1_F32 ? 4 : 2);
-    return kMallKeepBytes / chunk_bytes / 8;
+    const int64_t keep = kMallKeepBytes / chunk_bytes;
+    return table->nchunks > keep ? table->nchunks - keep : 0;
 }
 
 // The norm kernel over the table, then, with a tail, the one-workgroup final reduction + scalar chain.  (A single
@@ -1004,13 +1007,13 @@ static int launch_sumsq(const z1_table* table, double* partials, const z1_update
     int rc = check_table_device(table, &dev);
     if (rc) return rc;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const int64_t kpe = keep_per_eighth(table);
+    const int64_t kf = keep_from(table);
     if (table->g_dtype == Z1_F32)
         hipLaunchKernelGGL(sumsq_kernel<Z1_F32>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows_dev, table->nchunks, kpe, partials);
+                           table->nrows_dev, table->nchunks, kf, partials);
     else
         hipLaunchKernelGGL(sumsq_kernel<Z1_BF16>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows_dev, table->nchunks, kpe, partials);
+                           table->nrows_dev, table->nchunks, kf, partials);
     rc = launch_status();
     if (rc || !tail) return rc;
     hipLaunchKernelGGL(scalars_kernel, dim3(1), dim3(kThreads), 0, s, partials, *tail);
