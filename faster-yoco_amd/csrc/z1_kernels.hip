@@ -8,14 +8,14 @@
 //   * Adam + BF16: one wave per chunk, one wave per workgroup, dispatched by the hardware (grid = chunks).
 //     Workgroup b takes the b-th chunk from the end, so the hardware's round-robin dispatch over the 8 XCDs
 //     interleaves consecutive chunks over all XCDs, and all of them start on the MALL-resident end of the shard
-//     (see the MALL note below); a dynamic LDS reservation the kernel does not touch caps it at 16 resident
-//     workgroups per CU.  Measured on MI355X (431M-element shard): 2.02-2.03 ms, against 2.05 ms when each XCD
-//     streams one contiguous eighth, 2.52 ms for a persistent grid with a static partition (tail imbalance
-//     across CUs/XCDs) and 2.19 ms for 1024-element workgroups; the same kernel with its arithmetic
-//     replaced by additions runs at the same speed, i.e. it is at the bandwidth this 4-read / 4-write stream
-//     pattern reaches.  A launch covers a chunk range: the whole table, or the chunks of a range of rows
-//     (z1_adam_cast_rows), so a step can be cut into launches whose finished rows are sent while the rest runs
-//     (2 or 4 ranges of C2 cost nothing measurable, 8 cost 13 us).
+//     (see the MALL note below); a dynamic LDS reservation the kernel does not touch caps it at 12 resident
+//     workgroups per CU.  Measured on MI355X (431M-element shard): 1.93 ms, against 2.03 ms at 16 per CU,
+//     2.05 ms when each XCD streams one contiguous eighth (its best cap, 16), 2.52 ms for a persistent grid
+//     with a static partition (tail imbalance across CUs/XCDs) and 2.19 ms for 1024-element workgroups; the
+//     same kernel with its arithmetic replaced by additions ran at the same speed (the divisions and square
+//     roots are hidden under the memory traffic).  A launch covers a chunk range: the whole table, or the
+//     chunks of a range of rows (z1_adam_cast_rows), so a step can be cut into launches whose finished rows are
+//     sent while the rest runs (2 or 4 ranges of C2 cost nothing measurable, 8 cost 13 us).
 //   * Each lane moves one 128-bit group per fp32 array (and 64 bits of bf16); a wave instruction covers 1 KiB
 //     (fp32) or 512 B (bf16) of contiguous bytes, with nontemporal hints (streams far larger than L2 and MALL).
 //     The last, partial chunk of a row (and rows whose pointers are not aligned for the vector path) run an
@@ -69,8 +69,8 @@ constexpr int64_t kChunk = (int64_t)kWave * kVec * kGroups;   // elements per ch
 // 232-240 MB slower), its allocating stores costing more than the norm's allocating loads.
 constexpr int64_t kMallKeepBytes = 256ll << 20;
 constexpr int64_t kOwnerSumKeepBytes = 224ll << 20;
-constexpr int kAdamWgPerCu = 16;                              // resident Adam workgroups per CU (occupancy_lds)
-constexpr int kOwnerSumWgPerCu = 11;                          // resident owner-sum workgroups per CU
+constexpr int kAdamWgPerCu = 12;                              // resident Adam workgroups per CU (occupancy_lds)
+constexpr int kOwnerSumWgPerCu = 10;                          // resident owner-sum workgroups per CU
 constexpr int kMaxDevices = 64;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -695,8 +695,9 @@ int current_device(int* dev) {
 
 // Dynamic LDS a launch reserves (the kernels do not touch it) so that at most `per_cu` of its workgroups are
 // resident on one CU: the streaming kernels move HBM faster with fewer requests in flight (MI355X, 160 KiB of LDS
-// per CU: Adam 2.081 -> 2.038 ms at 16 one-wave workgroups per CU instead of the 32 the waves allow; 13 or fewer
-// and 20 or more are slower).  0 when the device does not report its LDS size.
+// per CU; C2 update, interleaved A/B runs on one box: Adam 1.93 ms at 11-12 one-wave workgroups per CU, 1.96 at
+// 13, 1.99 at 10 and 14, 2.03 at 16, 2.04-2.09 at 20-24, 2.10 at 8, 2.79 at 6; owner sum on C3 1.215-1.23 ms at
+// 9-11, 1.23 at 8, 1.42 at 6).  0 when the device does not report its LDS size.
 int occupancy_lds(int dev, int per_cu, size_t* bytes) {
     if (dev < 0 || dev >= kMaxDevices || per_cu < 1) return Z1_E_DEVICE;
     std::lock_guard<std::mutex> lk(g_mu);
