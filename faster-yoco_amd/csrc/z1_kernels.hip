@@ -70,6 +70,7 @@ constexpr int64_t kChunk = (int64_t)kWave * kVec * kGroups;   // elements per ch
 constexpr int64_t kMallKeepBytes = 256ll << 20;
 constexpr int64_t kOwnerSumKeepBytes = 224ll << 20;
 constexpr int kAdamWgPerCu = 12;                              // resident Adam workgroups per CU (occupancy_lds)
+constexpr int kAdamGoutWgPerCu = 11;                          // the same, with FP32 gradient outputs (5 write streams)
 constexpr int kOwnerSumWgPerCu = 10;                          // resident owner-sum workgroups per CU
 constexpr int kMaxDevices = 64;
 
@@ -696,8 +697,9 @@ int current_device(int* dev) {
 // Dynamic LDS a launch reserves (the kernels do not touch it) so that at most `per_cu` of its workgroups are
 // resident on one CU: the streaming kernels move HBM faster with fewer requests in flight (MI355X, 160 KiB of LDS
 // per CU; C2 update, interleaved A/B runs on one box: Adam 1.93 ms at 11-12 one-wave workgroups per CU, 1.96 at
-// 13, 1.99 at 10 and 14, 2.03 at 16, 2.04-2.09 at 20-24, 2.10 at 8, 2.79 at 6; owner sum on C3 1.215-1.23 ms at
-// 9-11, 1.23 at 8, 1.42 at 6).  0 when the device does not report its LDS size.
+// 13, 1.99 at 10 and 14, 2.03 at 16, 2.04-2.09 at 20-24, 2.10 at 8, 2.79 at 6; with FP32 gradient outputs, 38
+// per-parameter tensors: 2.15-2.17 ms at 11, 2.17-2.19 at 9-10, 2.19-2.23 at 12, 2.27-2.45 at 8 and 14-16; owner
+// sum on C3 1.215-1.23 ms at 9-11, 1.23 at 8, 1.42 at 6).  0 when the device does not report its LDS size.
 int occupancy_lds(int dev, int per_cu, size_t* bytes) {
     if (dev < 0 || dev >= kMaxDevices || per_cu < 1) return Z1_E_DEVICE;
     std::lock_guard<std::mutex> lk(g_mu);
@@ -1096,8 +1098,9 @@ static int adam_launch(const z1_table* table, int64_t chunk_begin, int64_t chunk
     k.omb2 = 1.0f - beta2;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const dim3 grid((unsigned)((chunk_end - chunk_begin + kAdamWaves - 1) / kAdamWaves));
+    const bool gout = table->gout_rows > 0;
     size_t lds = 0;
-    rc = occupancy_lds(dev, kAdamWgPerCu, &lds);
+    rc = occupancy_lds(dev, gout ? kAdamGoutWgPerCu : kAdamWgPerCu, &lds);
     if (rc) return rc;
 #define Z1_LAUNCH_ADAM(GDT, MODE, GOUT)                                                                        \
     hipLaunchKernelGGL((adam_cast_kernel<GDT, MODE, GOUT>), grid, dim3(kWave * kAdamWaves), lds, s, table->rows, \
@@ -1105,7 +1108,6 @@ static int adam_launch(const z1_table* table, int64_t chunk_begin, int64_t chunk
 #define Z1_LAUNCH_ADAM_MODES(GDT, GOUT)                                                                        \
     if (mode == 1) Z1_LAUNCH_ADAM(GDT, 1, GOUT);                                                              \
     else Z1_LAUNCH_ADAM(GDT, 0, GOUT)
-    const bool gout = table->gout_rows > 0;
     if (table->g_dtype == Z1_F32) {
         if (gout) { Z1_LAUNCH_ADAM_MODES(Z1_F32, true); }
         else { Z1_LAUNCH_ADAM_MODES(Z1_F32, false); }
