@@ -117,6 +117,46 @@ def test_dropin_fused_adam_cast_full_size_matches_oracle_digest(pkg, dev):
     assert got == {key: d['sha256'][key] for key in ('p', 'm', 'v', 'p16')}
 
 
+def test_dropin_folded_written_full_size_matches_c3_digest(pkg, dev):
+    """The drop-in's default step at full size: zero1_fast.step with the fused Adam hands FusedAdamCast the BF16
+    gradients to fold in (times the clip factor) and the FP32 gradient tensors to write, as the reference's scale
+    pass would have written them before its Adam (yoco/tasks/zero1_fast.py:175-195, fused_adam_cast.py:75-89).
+    On C3's inputs -- the owner sum of the 8 hashed contributions, its norm and clip factor -- over the 38 tensors
+    as per-parameter views, p, m, v and the BF16 copy must give C3's digests, and every written FP32 gradient must
+    equal torch's fp32 product of the BF16 average and the factor."""
+    from faster_yoco_amd import configs, shard as shard_mod
+    from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+    with open(os.path.join(HERE, 'large_digests.json')) as f:
+        d = json.load(f)['c3']
+    h = d['hparams']
+    sh = shard_mod.FlatShard(configs.shapes('c3'), dev, grad_dtype=torch.bfloat16)
+    assert sh.total == sh.numel == d['params']
+    contribs = configs.fill_shard_hashed(sh, 'c3')
+    opt = shard_mod.Zero1ShardOptimizer(sh, lr=h['lr'], betas=(h['beta1'], h['beta2']), eps=h['eps'],
+                                        weight_decay=h['weight_decay'])
+    opt.reduce_grads(contribs)
+    del contribs
+    gn = opt.clip_grad_norm(d['max_norm'])
+    fac = opt._multiply_factor.reshape(1).clone()
+    torch.cuda.synchronize()
+    assert (hexbits(opt._norm), hexbits(gn), hexbits(fac)) == (d['norm_bits'], d['grad_norm_bits'],
+                                                                d['factor_bits'])
+    ps, ms, vs, g16s, p16s = (sh.views(b) for b in ('p', 'm', 'v', 'g', 'p16'))
+    g32s = [torch.full(t.shape, float('nan'), dtype=torch.float32, device=dev) for t in ps]
+    fa = FusedAdamCast({p.data_ptr(): q for p, q in zip(ps, p16s)})
+    fa.fold, fa.fold_factor, fa.fold_writes = {p.data_ptr(): g for p, g in zip(ps, g16s)}, fac, True
+    noop = torch.zeros(1, dtype=torch.int32, device=dev)
+    fa(2048 * 32, noop, [g32s, ps, ms, vs], h['lr'], h['beta1'], h['beta2'], h['eps'], d['step'], 1, 1,
+       h['weight_decay'])
+    torch.cuda.synchronize()
+    assert len(fa.cast) == len(ps)
+    got = {k: digest(getattr(sh, k)) for k in ('p', 'm', 'v', 'p16')}
+    got['avg16'] = digest(sh.g)
+    assert got == d['sha256']
+    for g16, g32 in zip(g16s, g32s):
+        assert torch.equal((g16.float() * fac).view(torch.int32), g32.view(torch.int32))
+
+
 def test_dropin_ce_sum_slots_full_size_matches_oracle_digest(pkg, dev):
     """The copy-engine path's owner sum at C3's full size through the drop-in of CEReduce._sum
     (yoco/models/decoder/ce_reduce.py:59-74,178-183): rank 3's own contribution in OUT, the seven peers' in the
