@@ -412,7 +412,7 @@ def main():
         'kernel_ms': {'adam_cast': round(adam_avg, 4),
                       ('owner_sum+norm_clip' if cfg == 'c3' else 'norm_clip'):
                           round(sum(pre_ms) / len(pre_ms), 4)},
-        'roofline': {'bound': 'hbm', 'kernel': 'adam_cast_kernel', 'achieved': round(achieved, 1),
+        'roofline': {'bound': 'hbm', 'kernel': 'adam_flat_kernel', 'achieved': round(achieved, 1),
                      'peak': PEAK_HBM_GBPS, 'unit': 'GB/s', 'frac': round(achieved / PEAK_HBM_GBPS, 4),
                      'traffic': load_traffic('adam_cast', cfg),
                      'traffic_source': (traffic_file('adam_cast', cfg) + ' (rocprofv3 --pmc, committed; not measured '

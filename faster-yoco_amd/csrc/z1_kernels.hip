@@ -15,7 +15,10 @@
 //     same kernel with its arithmetic replaced by additions ran at the same speed (the divisions and square
 //     roots are hidden under the memory traffic).  A launch covers a chunk range: the whole table, or the
 //     chunks of a range of rows (z1_adam_cast_rows), so a step can be cut into launches whose finished rows are
-//     sent while the rest runs (2 or 4 ranges of C2 cost nothing measurable, 8 cost 13 us).
+//     sent while the rest runs (2 or 4 ranges of C2 cost nothing measurable, 8 cost 13 us).  When the rows tile
+//     one allocation per stream (the flat shard), a whole-table launch walks the buffers directly
+//     (adam_flat_kernel, 11 resident workgroups per CU): the same chunks' arithmetic without the two scalar
+//     lookups that start each wave, 2.175-2.177 against 2.185-2.188 ms per C2 update.
 //   * Each lane moves one 128-bit group per fp32 array (and 64 bits of bf16); a wave instruction covers 1 KiB
 //     (fp32) or 512 B (bf16) of contiguous bytes, with nontemporal hints (streams far larger than L2 and MALL).
 //     The last, partial chunk of a row (and rows whose pointers are not aligned for the vector path) run an
@@ -71,6 +74,7 @@ constexpr int64_t kMallKeepBytes = 256ll << 20;
 constexpr int64_t kOwnerSumKeepBytes = 224ll << 20;
 constexpr int kAdamWgPerCu = 12;                              // resident Adam workgroups per CU (occupancy_lds)
 constexpr int kAdamGoutWgPerCu = 11;                          // the same, with FP32 gradient outputs (5 write streams)
+constexpr int kAdamFlatWgPerCu = 11;                          // the same, over contiguous flat buffers
 constexpr int kOwnerSumWgPerCu = 10;                          // resident owner-sum workgroups per CU
 constexpr int kMaxDevices = 64;
 
@@ -191,28 +195,10 @@ __device__ __forceinline__ float load_g1(const void* g, int64_t i) {
 // GOUT: the table carries FP32 gradient outputs (z1_table_set_grad_out): each row's g' = fp32(g * factor), the value
 // the update consumes, is also stored to gout[row] (NULL: not for that row) -- the FP32 gradient the reference's
 // scale pass writes before its Adam reads it back (yoco/tasks/zero1_fast.py:175-192, fused_adam_cast.py:75-89).
+// One chunk of a row: elements [base, base + min(r.n - base, kChunk)) of r; the vector path when the chunk is whole
+// and the row's pointers are aligned, else an element-wise loop.
 template <int GDT, int MODE, bool GOUT>
-__global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row* __restrict__ rows,
-                                                                       const int32_t* __restrict__ chunk_row,
-                                                                       int64_t chunk_begin, int64_t chunk_end,
-                                                                       const float* __restrict__ factor,
-                                                                       const float* __restrict__ bc, AdamK k,
-                                                                       float* const* __restrict__ gout) {
-    const int lane = threadIdx.x & (kWave - 1);
-    // chunks [chunk_begin, chunk_end), last chunk first: the end of the gradient is what the pass before left in
-    // the MALL.  Consecutive workgroups take consecutive chunks and land on consecutive XCDs.
-    const int64_t c = chunk_end - 1 - ((int64_t)blockIdx.x * kAdamWaves +
-                                       __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
-    if (c < chunk_begin) return;
-    const float f = factor ? *factor : 1.0f;
-    if (bc) {                                   // bias corrections from device memory (z1_adam_cast_dev)
-        k.bc1 = bc[0];
-        k.bc2 = bc[1];
-    }
-    const int32_t ri = chunk_row[c];
-    const Row r = rows[ri];
-    float* const go = GOUT ? gout[ri] : nullptr;
-    const int64_t base = (c - r.chunk0) * kChunk;
+__device__ __forceinline__ void adam_chunk(const Row& r, float* go, int64_t base, int lane, float f, const AdamK& k) {
     const int64_t rem = r.n - base;
     if (rem >= kChunk && (r.vec & kVecAll) && (!GOUT || (reinterpret_cast<uintptr_t>(go) & 15) == 0)) {
         f4 g[kGroups], p[kGroups], m[kGroups], v[kGroups];
@@ -261,6 +247,47 @@ __global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row
             if (r.p16) r.p16[i] = (uint16_t)f32_to_bf16(pj);
         }
     }
+}
+
+template <int GDT, int MODE, bool GOUT>
+__global__ __launch_bounds__(kWave * kAdamWaves) void adam_cast_kernel(const Row* __restrict__ rows,
+                                                                       const int32_t* __restrict__ chunk_row,
+                                                                       int64_t chunk_begin, int64_t chunk_end,
+                                                                       const float* __restrict__ factor,
+                                                                       const float* __restrict__ bc, AdamK k,
+                                                                       float* const* __restrict__ gout) {
+    const int lane = threadIdx.x & (kWave - 1);
+    // chunks [chunk_begin, chunk_end), last chunk first: the end of the gradient is what the pass before left in
+    // the MALL.  Consecutive workgroups take consecutive chunks and land on consecutive XCDs.
+    const int64_t c = chunk_end - 1 - ((int64_t)blockIdx.x * kAdamWaves +
+                                       __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
+    if (c < chunk_begin) return;
+    const float f = factor ? *factor : 1.0f;
+    if (bc) {                                   // bias corrections from device memory (z1_adam_cast_dev)
+        k.bc1 = bc[0];
+        k.bc2 = bc[1];
+    }
+    const int32_t ri = chunk_row[c];
+    const Row r = rows[ri];
+    adam_chunk<GDT, MODE, GOUT>(r, GOUT ? gout[ri] : nullptr, (c - r.chunk0) * kChunk, lane, f, k);
+}
+
+// The same update when the table's rows tile one allocation per stream in order, without gaps (the flat shard:
+// z1_table marks it contiguous): Adam is element by element, so chunk c of the launch is elements
+// [c * kChunk, (c + 1) * kChunk) of the buffers of `w` (the first row's pointers, n = all elements), found without
+// the two scalar lookups (chunk -> row map, then the row) that start each wave of adam_cast_kernel.  Last chunk
+// first, as there.
+template <int GDT, int MODE>
+__global__ __launch_bounds__(kWave) void adam_flat_kernel(Row w, int64_t nchunks, const float* __restrict__ factor,
+                                                          const float* __restrict__ bc, AdamK k) {
+    const int lane = threadIdx.x;
+    const int64_t c = nchunks - 1 - (int64_t)blockIdx.x;
+    const float f = factor ? *factor : 1.0f;
+    if (bc) {
+        k.bc1 = bc[0];
+        k.bc2 = bc[1];
+    }
+    adam_chunk<GDT, MODE, false>(w, nullptr, c * kChunk, lane, f, k);
 }
 
 // -------------------------------------------------------------------------------------- deterministic norm
@@ -763,11 +790,46 @@ struct z1_table {
     float** gout;         // device, in the same allocation: the output of each device row (NULL: none)
     int64_t numel;
     int64_t nchunks;
+    std::vector<Row> host_rows;   // host copy of the device rows' pointers, kept by rebind / set_grads
+    int host_valid;       // 0 once a rebind / set_grads launch failed: the device rows may differ from host_rows
+    int contig;           // the device rows tile one allocation per stream in order, without gaps (see set_contig)
+    Row whole;            // when contig: the first row's pointers, n = numel, the vector flags of the whole
 };
 
 namespace z1detail {
 int occupancy_lds(int dev, int per_cu, size_t* bytes) { return ::occupancy_lds(dev, per_cu, bytes); }
 }  // namespace z1detail
+
+// Whether the table's rows, as the host last bound them, are one flat allocation per stream: row i's g, p, m, v
+// (and p16, if any row has one) start where row i - 1's end, every row has p, m and v, and the first row's pointers
+// are aligned for the vector path.  Then a whole-table Adam launch walks the buffers directly (adam_flat_kernel).
+static void set_contig(z1_table* t) {
+    t->contig = 0;
+    const std::vector<Row>& h = t->host_rows;
+    if (!t->host_valid || h.empty() || !t->has_pmv) return;
+    const Row& r0 = h[0];
+    const bool with16 = r0.p16 != nullptr;
+    const uintptr_t gsz = t->g_dtype == Z1_F32 ? 4 : 2;
+    const uintptr_t g0 = reinterpret_cast<uintptr_t>(r0.g), p0 = reinterpret_cast<uintptr_t>(r0.p),
+                    m0 = reinterpret_cast<uintptr_t>(r0.m), v0 = reinterpret_cast<uintptr_t>(r0.v),
+                    h0 = reinterpret_cast<uintptr_t>(r0.p16);
+    if ((g0 & (gsz == 4 ? 15 : 7)) || ((p0 | m0 | v0) & 15) || (h0 & 7)) return;
+    uintptr_t off = 0;                                 // elements before row i
+    for (const Row& r : h) {
+        if ((r.p16 != nullptr) != with16) return;
+        if (reinterpret_cast<uintptr_t>(r.g) != g0 + off * gsz || reinterpret_cast<uintptr_t>(r.p) != p0 + off * 4 ||
+            reinterpret_cast<uintptr_t>(r.m) != m0 + off * 4 || reinterpret_cast<uintptr_t>(r.v) != v0 + off * 4 ||
+            (with16 && reinterpret_cast<uintptr_t>(r.p16) != h0 + off * 2))
+            return;
+        off += (uintptr_t)r.n;
+    }
+    t->whole = r0;
+    t->whole.n = (int64_t)off;
+    t->whole.chunk0 = 0;
+    t->whole.pmv_aligned = 1;
+    t->whole.vec = kVecG | kVecAll;
+    t->contig = 1;
+}
 
 extern "C" {
 
@@ -846,6 +908,9 @@ static int table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table*
     tb->first_chunk.swap(first);
     tb->dev_row.swap(dev_row);
     tb->row_numel.swap(row_numel);
+    tb->host_rows = h;
+    tb->host_valid = 1;
+    set_contig(tb);
     tb->rows = nullptr;
     hipError_t e = hipMalloc(reinterpret_cast<void**>(&tb->rows), img.size());
     if (e != hipSuccess) {
@@ -906,6 +971,16 @@ int z1_table_rebind(z1_table* table, const z1_tensor* rows, int nrows, void* str
     memset(&b, 0, sizeof(b));
     b.g_align = table->g_dtype == Z1_F32 ? 16 : 8;
     hipStream_t s = static_cast<hipStream_t>(stream);
+    table->contig = 0;                                 // until every rebind launch is enqueued
+    for (int i = 0; i < nrows; ++i) {
+        if (table->dev_row[i] < 0) continue;
+        Row& hr = table->host_rows[table->dev_row[i]];
+        hr.g = rows[i].g;
+        hr.p = rows[i].p;
+        hr.m = rows[i].m;
+        hr.v = rows[i].v;
+        hr.p16 = rows[i].p16;
+    }
     for (int i = 0; i < nrows; ++i) {
         if (table->dev_row[i] < 0) continue;
         const int k = b.count;
@@ -918,14 +993,22 @@ int z1_table_rebind(z1_table* table, const z1_tensor* rows, int nrows, void* str
         if (++b.count == kRebindPerLaunch) {
             hipLaunchKernelGGL(rebind_rows_kernel, dim3(1), dim3(kRebindPerLaunch), 0, s, table->rows, b);
             rc = launch_status();
-            if (rc) return rc;
+            if (rc) {
+                table->host_valid = 0;
+                return rc;
+            }
             b.count = 0;
         }
     }
     if (b.count) {
         hipLaunchKernelGGL(rebind_rows_kernel, dim3(1), dim3(kRebindPerLaunch), 0, s, table->rows, b);
-        return launch_status();
+        rc = launch_status();
+        if (rc) {
+            table->host_valid = 0;
+            return rc;
+        }
     }
+    set_contig(table);
     return Z1_OK;
 }
 
@@ -943,6 +1026,9 @@ int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* s
         if (table->dev_row[i] < 0) continue;
         if (!g[i]) return Z1_E_NULL;
     }
+    table->contig = 0;                                 // until every binding launch is enqueued
+    for (int i = 0; i < nrows; ++i)
+        if (table->dev_row[i] >= 0) table->host_rows[table->dev_row[i]].g = g[i];
     for (int i = 0; i < nrows; ++i) {
         if (table->dev_row[i] < 0) continue;
         b.g[b.count] = g[i];
@@ -950,14 +1036,22 @@ int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* s
         if (++b.count == kBindPerLaunch) {
             hipLaunchKernelGGL(set_grads_kernel, dim3(1), dim3(kBindPerLaunch), 0, s, table->rows, b);
             rc = launch_status();
-            if (rc) return rc;
+            if (rc) {
+                table->host_valid = 0;
+                return rc;
+            }
             b.count = 0;
         }
     }
     if (b.count) {
         hipLaunchKernelGGL(set_grads_kernel, dim3(1), dim3(kBindPerLaunch), 0, s, table->rows, b);
-        return launch_status();
+        rc = launch_status();
+        if (rc) {
+            table->host_valid = 0;
+            return rc;
+        }
     }
+    set_contig(table);
     return Z1_OK;
 }
 
@@ -1097,9 +1191,26 @@ static int adam_launch(const z1_table* table, int64_t chunk_begin, int64_t chunk
     k.omb1 = 1.0f - beta1;
     k.omb2 = 1.0f - beta2;
     hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid((unsigned)((chunk_end - chunk_begin + kAdamWaves - 1) / kAdamWaves));
     const bool gout = table->gout_rows > 0;
     size_t lds = 0;
+    if (table->contig && !gout && chunk_begin == 0 && chunk_end == table->nchunks) {   // the whole flat shard
+        const int64_t nflat = (table->whole.n + kChunk - 1) / kChunk;
+        rc = occupancy_lds(dev, kAdamFlatWgPerCu, &lds);
+        if (rc) return rc;
+#define Z1_LAUNCH_ADAM_FLAT(GDT, MODE)                                                                        \
+    hipLaunchKernelGGL((adam_flat_kernel<GDT, MODE>), dim3((unsigned)nflat), dim3(kWave), lds, s, table->whole, \
+                       nflat, factor, bc, k)
+        if (table->g_dtype == Z1_F32) {
+            if (mode == 1) Z1_LAUNCH_ADAM_FLAT(Z1_F32, 1);
+            else Z1_LAUNCH_ADAM_FLAT(Z1_F32, 0);
+        } else {
+            if (mode == 1) Z1_LAUNCH_ADAM_FLAT(Z1_BF16, 1);
+            else Z1_LAUNCH_ADAM_FLAT(Z1_BF16, 0);
+        }
+#undef Z1_LAUNCH_ADAM_FLAT
+        return launch_status();
+    }
+    const dim3 grid((unsigned)((chunk_end - chunk_begin + kAdamWaves - 1) / kAdamWaves));
     rc = occupancy_lds(dev, gout ? kAdamGoutWgPerCu : kAdamWgPerCu, &lds);
     if (rc) return rc;
 #define Z1_LAUNCH_ADAM(GDT, MODE, GOUT)                                                                        \

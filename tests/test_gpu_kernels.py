@@ -122,6 +122,86 @@ def test_adam_misaligned_rows_use_the_element_path(pkg, dev):
         check_rows(rows, got, False, 0.75, 10)
 
 
+def flat_rows(rows_np, g_bf16, dev, with_p16=True):
+    """The rows in one allocation per stream, in order and without gaps (the flat shard's layout): the flat
+    buffers and per-row views of them."""
+    cat = lambda k: np.concatenate([r[k] for r in rows_np])
+    G = dev_bf16(cat(0), dev) if g_bf16 else dev_f32(cat(0), dev)
+    P, M, V = dev_f32(cat(1), dev), dev_f32(cat(2), dev), dev_f32(cat(3), dev)
+    P16 = torch.zeros(P.numel(), dtype=torch.bfloat16, device=dev) if with_p16 else None
+    views, off = [], 0
+    for r in rows_np:
+        n = r[1].size
+        sl = slice(off, off + n)
+        views.append((G[sl], P[sl], M[sl], V[sl], P16[sl] if with_p16 else None, n))
+        off += n
+    return (G, P, M, V, P16), views
+
+
+def host_rows(views):
+    return [(host_f32(p), host_f32(m), host_f32(v), host_bf16(p16) if p16 is not None else None)
+            for _, p, m, v, p16, _ in views]
+
+
+@pytest.mark.parametrize('with_p16', [True, False])
+@pytest.mark.parametrize('mode', [1, 0])
+@pytest.mark.parametrize('g_bf16', [False, True])
+def test_adam_contiguous_rows_take_the_flat_launch(pkg, dev, g_bf16, mode, with_p16):
+    """Rows that tile one allocation per stream in order (the flat shard) are updated by the launch that walks the
+    buffers directly; its chunks straddle the rows' boundaries where sizes are not multiples of 256.  Bit-exact
+    against the oracle, as the table walk over the same rows in separate allocations is."""
+    from faster_yoco_amd import ops
+    sizes = [1000, 333, 4096, 7777, 256, 5, 70001]
+    rows = []
+    for i, n in enumerate(sizes):
+        g, p, m, v = rand_state(n, 500 + i)
+        rows.append((oracle.bf16_rne(g) if g_bf16 else g, p, m, v))
+    (G, P, M, V, P16), views = flat_rows(rows, g_bf16, dev, with_p16)
+    offsets = np.concatenate([[0], np.cumsum(sizes)[:-1]]).tolist()
+    table = ops.Table.flat(offsets, sizes, G, P, M, V, P16)
+    bc1, bc2 = ops.bias_corrections(HP['beta1'], HP['beta2'], 7)
+    f = torch.tensor([0.625], dtype=torch.float32, device=dev)
+    ops.adam_cast(table, f, HP['lr'], HP['beta1'], HP['beta2'], HP['eps'], bc1, bc2, HP['weight_decay'], mode)
+    torch.cuda.synchronize()
+    got = host_rows(views)
+    check_rows(rows, got, g_bf16, 0.625, 7, mode)
+    table.close()
+    sep = run_adam_rows(pkg, dev, rows, g_bf16, factor=0.625, step=7, mode=mode, with_p16=with_p16)
+    for a, b in zip(got, sep):
+        assert all(same_f32(x, y) for x, y in zip(a[:3], b[:3]))
+        assert (a[3] is None) == (b[3] is None) and (a[3] is None or same_bf16(a[3], b[3]))
+
+
+def test_adam_table_rebound_between_flat_and_separate_rows(pkg, dev):
+    """One list table bound in turn to views of flat buffers (the launch that walks the buffers), to separately
+    allocated tensors (the table walk), and to the flat views again: every update bit-exact against the oracle.
+    Whether a launch may walk the buffers directly follows the addresses of each call."""
+    from faster_yoco_amd import ops
+    sizes = [3000, 1, 4096 + 17, 513]
+    rows = [rand_state(n, 600 + i) for i, n in enumerate(sizes)]
+    _, views = flat_rows(rows, False, dev)
+    sep = [(dev_f32(g, dev), dev_f32(p, dev), dev_f32(m, dev), dev_f32(v, dev),
+            torch.zeros(p.size, dtype=torch.bfloat16, device=dev), p.size) for g, p, m, v in rows]
+    table = ops.Table(sep, dev)
+    bc1, bc2 = ops.bias_corrections(HP['beta1'], HP['beta2'], 3)
+    want = rows
+    for k, bound in enumerate((views, sep, views)):
+        ops.adam_cast(table, None, HP['lr'], HP['beta1'], HP['beta2'], HP['eps'], bc1, bc2, HP['weight_decay'], 1,
+                      tensors=ops.rows_lists(bound))
+        torch.cuda.synchronize()
+        got = host_rows(bound)
+        check_rows(want, got, False, None, 3)
+        # the next binding's inputs: these outputs (p, m, v) with the same gradients
+        want = [(g, gp, gm, gv) for (g, _, _, _), (gp, gm, gv, _) in zip(rows, got)]
+        if k < 2:
+            nxt = (sep, views)[k]
+            for (_, p, m, v, _, _), (gp, gm, gv, _) in zip(nxt, got):
+                p.copy_(torch.from_numpy(gp))
+                m.copy_(torch.from_numpy(gm))
+                v.copy_(torch.from_numpy(gv))
+    table.close()
+
+
 def test_adam_without_bf16_copy_and_special_values(pkg, dev):
     n = 4096 * 2 + 100
     g, p, m, v = rand_state(n, 400)
