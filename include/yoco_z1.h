@@ -59,8 +59,11 @@ typedef struct z1_table z1_table;            /* opaque, device-resident table + 
 
 /* Builds the device copy of `rows` (plain copy of the pointers; rows with n == 0 are dropped) on the current
  * device.  The p, m, v and p16 ranges of different rows must not overlap (each element is updated by exactly one
- * lane; overlapping rows race).  Replaces the per-call tensor-list walk of yoco/tasks/fused_adam_cast.py:62-72 and the bucket/view
- * bookkeeping of yoco/tasks/zero1_fast.py:110-128 with one schedule built at set-up.  Allocates (hipMalloc). */
+ * lane; overlapping rows race).  Replaces the per-call tensor-list walk of yoco/tasks/fused_adam_cast.py:62-72 and
+ * the bucket/view bookkeeping of yoco/tasks/zero1_fast.py:110-128 with one schedule built at set-up.  When the
+ * rows, as last bound (here, z1_table_set_grads or z1_table_rebind), tile one allocation per stream in order and
+ * without gaps -- a flat shard -- and no gradient outputs are set, a whole-table Adam launch walks those buffers
+ * directly; the values are the same.  Allocates (hipMalloc). */
 int z1_table_create(const z1_tensor* rows, int nrows, int g_dtype, z1_table** out);
 /* Frees a table (hipFree, which first waits for the device's queued work, so launches already enqueued with the
  * table complete).  Not during stream capture; a captured graph whose launches use the table must not be replayed
