@@ -202,6 +202,33 @@ def test_adam_table_rebound_between_flat_and_separate_rows(pkg, dev):
     table.close()
 
 
+def test_adam_flat_rows_with_gradients_moved_apart(pkg, dev):
+    """A table over views of flat buffers whose gradients are then given as separate allocations (the operators
+    rebind only the gradient column, as when autograd reallocates gradients): the rows are no longer one allocation
+    per stream, so the launch walks the table; then the gradients move into another flat buffer and the launch walks
+    the buffers again.  Bit-exact against the oracle each time."""
+    from faster_yoco_amd import ops
+    sizes = [2048, 777, 4096, 300]
+    rows = [rand_state(n, 700 + i) for i, n in enumerate(sizes)]
+    (G, _, _, _, _), views = flat_rows(rows, False, dev)
+    table = ops.Table(views, dev)
+    bc1, bc2 = ops.bias_corrections(HP['beta1'], HP['beta2'], 5)
+    G2 = G.clone()
+    offsets = np.concatenate([[0], np.cumsum(sizes)[:-1]]).tolist()
+    want = rows
+    for grads in ([v[0] for v in views], [dev_f32(r[0], dev) for r in rows],
+                  [G2[o:o + n] for o, n in zip(offsets, sizes)]):
+        tensors = (grads, [v[1] for v in views], [v[2] for v in views], [v[3] for v in views],
+                   [v[4] for v in views])
+        ops.adam_cast(table, None, HP['lr'], HP['beta1'], HP['beta2'], HP['eps'], bc1, bc2, HP['weight_decay'], 1,
+                      tensors=tensors)
+        torch.cuda.synchronize()
+        got = host_rows(views)
+        check_rows(want, got, False, None, 5)
+        want = [(g, gp, gm, gv) for (g, _, _, _), (gp, gm, gv, _) in zip(rows, got)]
+    table.close()
+
+
 def test_adam_without_bf16_copy_and_special_values(pkg, dev):
     n = 4096 * 2 + 100
     g, p, m, v = rand_state(n, 400)
