@@ -75,7 +75,7 @@ constexpr int64_t kOwnerSumKeepBytes = 224ll << 20;
 constexpr int kAdamWgPerCu = 12;                              // resident Adam workgroups per CU (occupancy_lds)
 constexpr int kAdamGoutWgPerCu = 11;                          // the same, with FP32 gradient outputs (5 write streams)
 constexpr int kAdamFlatWgPerCu = 11;                          // the same, over contiguous flat buffers
-constexpr int kOwnerSumWgPerCu = 10;                          // resident owner-sum workgroups per CU
+constexpr int kOwnerSumWgPerCu = 16;                          // resident owner-sum workgroups per CU
 constexpr int kMaxDevices = 64;
 
 typedef float f4 __attribute__((ext_vector_type(4)));
@@ -503,57 +503,58 @@ struct Srcs {
     const uint16_t* p[Z1_MAX_WORLD];
 };
 
-// Owner sum: one wave per chunk of kSumChunk = 512 elements (8 per lane, 16 B per contribution), workgroup b on
-// chunk b, dispatched by the hardware round-robin over the XCDs (measured 6.2 TB/s for this 8-read / 1-write
-// pattern, against 6.0 TB/s with each XCD on one contiguous eighth and 4.5 TB/s for a static grid-stride
-// partition).  W is a compile-time constant so that all W loads of a lane are in flight together (a runtime count
-// makes the compiler wait on each load before issuing the next).  OUT may alias one source: every element is read
-// before the same lane writes it.  With wave_partials, lane 0 of each wave writes the FP64 sum of squares of its
-// chunk's rounded averages to wave_partials[chunk] (a fixed decomposition; the partials are then reduced in a
-// fixed order by reduce_partials_kernel).
-constexpr int64_t kSumChunk = (int64_t)kWave * 8;
+// Owner sum: one wave per chunk of kSumChunk = 256 elements (4 per lane, 8 B per contribution), workgroup b on
+// chunk b, dispatched by the hardware round-robin over the XCDs, at most 16 resident workgroups per CU.  Measured
+// at C3's size (8 contributions of 430,662,912 elements, throw-away probe of the same kernel): 1.201-1.204 ms at
+// 16-20 per CU against 1.221-1.234 ms for 512-element chunks with 16 B per lane at their best caps (10-12),
+// 1.38-1.41 ms for 128-element chunks (4 B per lane, 24-40 per CU); this 8-read / 1-write pattern ran at 6.0 TB/s
+// with each XCD on one contiguous eighth and 4.5 TB/s for a static grid-stride partition.  W is a compile-time
+// constant so that all W loads of a lane are in flight together (a runtime count makes the compiler wait on each
+// load before issuing the next).  OUT may alias one source: every element is read before the same lane writes it.
+// With wave_partials, lane 0 of each wave writes the FP64 sum of squares of its chunk's rounded averages to
+// wave_partials[chunk] (a fixed decomposition; the partials are then reduced in a fixed order by
+// reduce_partials_kernel).
+constexpr int kSumVec = 4;                                    // elements per lane and chunk
+constexpr int64_t kSumChunk = (int64_t)kWave * kSumVec;
 
 template <int W, bool KEEP>
 __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, float scale, uint16_t* out,
                                                           float* out_sum, double* wave_partials, int vec,
                                                           int64_t chunk_base) {
     const int64_t c = chunk_base + (int64_t)blockIdx.x;
-    const int64_t e0 = c * kSumChunk + (int64_t)threadIdx.x * 8;
+    const int64_t e0 = c * kSumChunk + (int64_t)threadIdx.x * kSumVec;
     double acc2 = 0.0;
-    if (vec && e0 + 8 <= n) {
-        const int64_t gi = e0 / 8;
-        u4 x[W];
+    if (vec && e0 + kSumVec <= n) {
+        const int64_t gi = e0 / kSumVec;
+        u2 x[W];
 #pragma unroll
-        for (int k = 0; k < W; ++k) x[k] = ld(reinterpret_cast<const u4*>(s.p[k]) + gi);
-        float a[8];
+        for (int k = 0; k < W; ++k) x[k] = ld(reinterpret_cast<const u2*>(s.p[k]) + gi);
+        float a[kSumVec];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = 0.0f;
+        for (int j = 0; j < kSumVec; ++j) a[j] = 0.0f;
 #pragma unroll
         for (int k = 0; k < W; ++k) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
+            for (int w = 0; w < kSumVec / 2; ++w) {
                 a[2 * w] = a[2 * w] + bf16_lo(x[k][w]);
                 a[2 * w + 1] = a[2 * w + 1] + bf16_hi(x[k][w]);
             }
         }
-        u4 o;
+        u2 o;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) o[w] = pack_bf16(a[2 * w] * scale, a[2 * w + 1] * scale);
-        if (KEEP) st_keep(reinterpret_cast<u4*>(out) + gi, o);
-        else st(reinterpret_cast<u4*>(out) + gi, o);
-        if (out_sum) {
-            st(reinterpret_cast<f4*>(out_sum) + 2 * gi, f4{a[0], a[1], a[2], a[3]});
-            st(reinterpret_cast<f4*>(out_sum) + 2 * gi + 1, f4{a[4], a[5], a[6], a[7]});
-        }
+        for (int w = 0; w < kSumVec / 2; ++w) o[w] = pack_bf16(a[2 * w] * scale, a[2 * w + 1] * scale);
+        if (KEEP) st_keep(reinterpret_cast<u2*>(out) + gi, o);
+        else st(reinterpret_cast<u2*>(out) + gi, o);
+        if (out_sum) st(reinterpret_cast<f4*>(out_sum) + gi, f4{a[0], a[1], a[2], a[3]});
         if (wave_partials) {
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
+            for (int w = 0; w < kSumVec / 2; ++w) {
                 acc2 += sq64(bf16_lo(o[w]));
                 acc2 += sq64(bf16_hi(o[w]));
             }
         }
     } else {
-        const int64_t e1 = e0 + 8 < n ? e0 + 8 : n;
+        const int64_t e1 = e0 + kSumVec < n ? e0 + kSumVec : n;
         for (int64_t e = e0; e < e1; ++e) {
             float a = 0.0f;
 #pragma unroll
@@ -750,7 +751,7 @@ inline int launch_status() {
 }  // namespace
 
 // Scratch of z1_owner_sum_update_noalloc: the norm's Z1_NORM_PARTIALS partials, then one per-wave partial per
-// owner-sum chunk, for up to Z1_NOALLOC_MAX_N elements (8.0 MiB; every device the library runs on holds its own copy
+// owner-sum chunk, for up to Z1_NOALLOC_MAX_N elements (16.0 MiB; every device the library runs on holds its own copy
 // until the process ends).  Host code never passes this name to a kernel: in host code it is a stand-in, not a
 // device address.  The address of a device's copy comes from hipGetSymbolAddress, once per device.
 constexpr int64_t kNoallocDoubles = Z1_NORM_PARTIALS + Z1_NOALLOC_MAX_N / kSumChunk;

@@ -163,7 +163,7 @@ int z1_owner_sum_update(const uint16_t* const* contrib, int world, int64_t n, fl
                         float* out_sum, double* workspace, const z1_update_scalars* u, void* stream);
 
 /* z1_owner_sum_update with its workspace in the library's own fixed device scratch (a static device array of
- * 8.0 MiB per device, held until the process ends): no allocation of any kind, so callers that cannot allocate --
+ * 16.0 MiB per device, held until the process ends): no allocation of any kind, so callers that cannot allocate --
  * code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc -- can run the owner sum, norm
  * and clip chain.  No counterpart in the reference.  n is at most Z1_NOALLOC_MAX_N (Z1_E_NOALLOC_MAX beyond; the
  * largest YOCO-3B owner shard is 443,357,184).  Every call on one device shares that device's scratch: calls that

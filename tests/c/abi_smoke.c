@@ -25,7 +25,7 @@ int main(void) {
         bad |= z1_table_create(r, 2, Z1_F32, &t) != Z1_E_SIZE;
         bad |= t != 0;
     }
-    bad |= z1_owner_sum_workspace(513) != Z1_NORM_PARTIALS + 2;       /* the partials, then one per chunk */
+    bad |= z1_owner_sum_workspace(513) != Z1_NORM_PARTIALS + 3;       /* the partials, then one per 256-element chunk */
     bad |= z1_grad_norm_clip(0, 0, 0, 1.f, 0, 0, 0, 1.f, 0) != Z1_E_NULL;
     bad |= z1_table_set_grads(0, 0, 0, 0) != Z1_E_NULL;
     bad |= z1_adam_cast(0, 0, 0.f, 0.f, 0.f, 0.f, 1.f, 1.f, 0.f, 1, 0) != Z1_E_NULL;

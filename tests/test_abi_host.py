@@ -67,7 +67,7 @@ def test_argument_errors_without_device_work(pkg):
     assert L.z1_cast_bf16(None, None, 4, None) == -1
     assert L.z1_table_destroy(None) == 0
     assert L.z1_owner_sum_workspace(-1) == -2
-    assert [L.z1_owner_sum_workspace(n) for n in (0, 1, 512, 513)] == [2048, 2049, 2049, 2050]
+    assert [L.z1_owner_sum_workspace(n) for n in (0, 1, 256, 257, 513)] == [2048, 2049, 2049, 2050, 2051]
     assert L.z1_grad_norm_clip(None, None, None, 1.0, None, None, None, 1.0, None) == -1
     assert L.z1_grad_update_scalars(None, None, None, None) == -1
     assert L.z1_table_set_grads(None, None, 0, None) == -1
