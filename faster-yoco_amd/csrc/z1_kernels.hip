@@ -511,9 +511,11 @@ struct Srcs {
 // with each XCD on one contiguous eighth and 4.5 TB/s for a static grid-stride partition.  W is a compile-time
 // constant so that all W loads of a lane are in flight together (a runtime count makes the compiler wait on each
 // load before issuing the next).  OUT may alias one source: every element is read before the same lane writes it.
-// With wave_partials, lane 0 of each wave writes the FP64 sum of squares of its chunk's rounded averages to
-// wave_partials[chunk] (a fixed decomposition; the partials are then reduced in a fixed order by
-// reduce_partials_kernel).
+// With wave_partials, lane 0 of each wave writes the FP64 sum of squares of its chunk's rounded averages to a slot
+// of its own (a fixed decomposition; the partials are then reduced in a fixed order by reduce_partials_kernel).
+// The slot is chunk_of_block of the workgroup, which places the partials of the workgroups one XCD runs next to
+// each other, so that XCD's L2 writes them back as whole lines (in chunk order, each partial left its L2 as a
+// write request of its own: 54 MB of 32-byte requests at C3's size).
 constexpr int kSumVec = 4;                                    // elements per lane and chunk
 constexpr int64_t kSumChunk = (int64_t)kWave * kSumVec;
 
@@ -568,7 +570,7 @@ __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, flo
     if (wave_partials) {
 #pragma unroll
         for (int off = kWave / 2; off > 0; off >>= 1) acc2 += __shfl_xor(acc2, off, kWave);
-        if (threadIdx.x == 0) wave_partials[c] = acc2;
+        if (threadIdx.x == 0) wave_partials[chunk_base + chunk_of_block(blockIdx.x, gridDim.x)] = acc2;
     }
 }
 
