@@ -105,15 +105,23 @@ void require_gpu(const Tensor& t, const char* what) {
 
 void* ptr(const OptTensor& t) { return t.has_value() && t->defined() ? t->data_ptr() : nullptr; }
 
-float* scalar_ptr(const OptTensor& t, const char* what) {
+// Every tensor a launch reads or writes must live on the launch's device: a pointer into another GPU's memory would
+// reach the kernel unchecked.
+void require_on(const Tensor& t, int device, const char* what) {
+    require_gpu(t, what);
+    TORCH_CHECK(t.device().index() == device, what, ": a tensor is on cuda:", static_cast<int>(t.device().index()),
+                ", the launch runs on cuda:", device);
+}
+
+float* scalar_ptr(const OptTensor& t, const char* what, int device) {
     if (!t.has_value() || !t->defined()) return nullptr;
-    require_gpu(*t, what);
+    require_on(*t, device, what);
     TORCH_CHECK(t->scalar_type() == at::kFloat && t->numel() == 1, what, ": expected a 1-element fp32 device tensor");
     return static_cast<float*>(t->data_ptr());
 }
 
-double* partials_ptr(const Tensor& t, const char* what, int64_t need = Z1_NORM_PARTIALS) {
-    require_gpu(t, what);
+double* partials_ptr(const Tensor& t, const char* what, int device, int64_t need = Z1_NORM_PARTIALS) {
+    require_on(t, device, what);
     TORCH_CHECK(t.scalar_type() == at::kDouble && t.numel() >= need && t.is_contiguous(),
                 "yoco_z1: the norm workspace must hold ", need, " float64");
     return static_cast<double*>(t.data_ptr());
@@ -121,27 +129,27 @@ double* partials_ptr(const Tensor& t, const char* what, int64_t need = Z1_NORM_P
 
 // z1_update_scalars: the factor is read from `factor` (in place) unless factor_value is given; then `factor`, if
 // given, only receives the clipped value.
-z1_update_scalars scalars(const char* what, const OptTensor& factor, std::optional<double> factor_value,
+z1_update_scalars scalars(const char* what, int device, const OptTensor& factor, std::optional<double> factor_value,
                           const OptTensor& norm, const OptTensor& grad_norm, const OptTensor& flags,
                           const OptTensor& clip_log, const OptTensor& sample_size, double numer, double max_norm) {
     uint8_t* fl = nullptr;
     if (flags.has_value() && flags->defined()) {
-        require_gpu(*flags, what);
+        require_on(*flags, device, what);
         TORCH_CHECK((flags->scalar_type() == at::kByte || flags->scalar_type() == at::kBool) && flags->numel() >= 2,
                     what, ": flags must hold 2 uint8/bool");
         fl = static_cast<uint8_t*>(flags->data_ptr());
     }
     z1_update_scalars u;
-    u.sample_size = scalar_ptr(sample_size, what);
+    u.sample_size = scalar_ptr(sample_size, what, device);
     u.numer = static_cast<float>(numer);
-    u.factor_in = factor_value.has_value() ? nullptr : scalar_ptr(factor, what);
+    u.factor_in = factor_value.has_value() ? nullptr : scalar_ptr(factor, what, device);
     u.factor_value = factor_value.has_value() ? static_cast<float>(*factor_value) : 1.0f;
     u.max_norm = static_cast<float>(max_norm);
-    u.norm_out = scalar_ptr(norm, what);
-    u.grad_norm_out = scalar_ptr(grad_norm, what);
-    u.factor_out = scalar_ptr(factor, what);
+    u.norm_out = scalar_ptr(norm, what, device);
+    u.grad_norm_out = scalar_ptr(grad_norm, what, device);
+    u.factor_out = scalar_ptr(factor, what, device);
     u.flags_out = fl;
-    u.clip_log_out = scalar_ptr(clip_log, what);
+    u.clip_log_out = scalar_ptr(clip_log, what, device);
     return u;
 }
 
@@ -294,28 +302,30 @@ struct OnDevice {
 
 // ------------------------------------------------------------------------------------------ norm and clip chain
 void grad_sumsq_(int64_t table, TensorList g, const Tensor& partials) {
-    double* part = partials_ptr(partials, "grad_sumsq");
     OnTable on(table);
+    double* part = partials_ptr(partials, "grad_sumsq", on.t.device);
     bind(on.t, g, nullptr, nullptr, "grad_sumsq", on.stream);
     check_rc(api().grad_sumsq(on.t.h, part, on.stream), "z1_grad_sumsq");
 }
 
 void norm_clip_(const Tensor& partials, const OptTensor& factor, const OptTensor& norm, const OptTensor& grad_norm,
                 double max_norm, std::optional<double> factor_value) {
-    double* part = partials_ptr(partials, "norm_clip");
-    z1_update_scalars u = scalars("norm_clip", factor, factor_value, norm, grad_norm, std::nullopt, std::nullopt,
-                                  std::nullopt, 1.0, max_norm);
+    require_gpu(partials, "norm_clip");
     OnDevice on(partials);
+    const int dev = partials.device().index();
+    double* part = partials_ptr(partials, "norm_clip", dev);
+    z1_update_scalars u = scalars("norm_clip", dev, factor, factor_value, norm, grad_norm, std::nullopt, std::nullopt,
+                                  std::nullopt, 1.0, max_norm);
     check_rc(api().update_scalars_run(part, &u, on.stream), "z1_norm_clip");
 }
 
 void grad_norm_clip_(int64_t table, TensorList g, const Tensor& partials, const OptTensor& factor,
                      const OptTensor& norm, const OptTensor& grad_norm, double max_norm,
                      std::optional<double> factor_value) {
-    double* part = partials_ptr(partials, "grad_norm_clip");
-    z1_update_scalars u = scalars("grad_norm_clip", factor, factor_value, norm, grad_norm, std::nullopt, std::nullopt,
-                                  std::nullopt, 1.0, max_norm);
     OnTable on(table);
+    double* part = partials_ptr(partials, "grad_norm_clip", on.t.device);
+    z1_update_scalars u = scalars("grad_norm_clip", on.t.device, factor, factor_value, norm, grad_norm, std::nullopt,
+                                  std::nullopt, std::nullopt, 1.0, max_norm);
     bind(on.t, g, nullptr, nullptr, "grad_norm_clip", on.stream);
     check_rc(api().grad_update_scalars(on.t.h, part, &u, on.stream), "z1_grad_norm_clip");
 }
@@ -324,10 +334,12 @@ void update_scalars_(const Tensor& partials, const OptTensor& factor, const OptT
                      const OptTensor& grad_norm, const OptTensor& flags, const OptTensor& clip_log,
                      const OptTensor& sample_size, double numer, double max_norm,
                      std::optional<double> factor_value) {
-    double* part = partials_ptr(partials, "update_scalars");
-    z1_update_scalars u = scalars("update_scalars", factor, factor_value, norm, grad_norm, flags, clip_log,
-                                  sample_size, numer, max_norm);
+    require_gpu(partials, "update_scalars");
     OnDevice on(partials);
+    const int dev = partials.device().index();
+    double* part = partials_ptr(partials, "update_scalars", dev);
+    z1_update_scalars u = scalars("update_scalars", dev, factor, factor_value, norm, grad_norm, flags, clip_log,
+                                  sample_size, numer, max_norm);
     check_rc(api().update_scalars_run(part, &u, on.stream), "z1_update_scalars");
 }
 
@@ -335,22 +347,25 @@ void grad_update_scalars_(int64_t table, TensorList g, const Tensor& partials, c
                           const OptTensor& norm, const OptTensor& grad_norm, const OptTensor& flags,
                           const OptTensor& clip_log, const OptTensor& sample_size, double numer, double max_norm,
                           std::optional<double> factor_value) {
-    double* part = partials_ptr(partials, "grad_update_scalars");
-    z1_update_scalars u = scalars("grad_update_scalars", factor, factor_value, norm, grad_norm, flags, clip_log,
-                                  sample_size, numer, max_norm);
     OnTable on(table);
+    double* part = partials_ptr(partials, "grad_update_scalars", on.t.device);
+    z1_update_scalars u = scalars("grad_update_scalars", on.t.device, factor, factor_value, norm, grad_norm, flags,
+                                  clip_log, sample_size, numer, max_norm);
     bind(on.t, g, nullptr, nullptr, "grad_update_scalars", on.stream);
     check_rc(api().grad_update_scalars(on.t.h, part, &u, on.stream), "z1_grad_update_scalars");
 }
 
 void clip_factor_(const Tensor& norm, const OptTensor& factor, const OptTensor& grad_norm, double max_norm,
                   std::optional<double> factor_value) {
-    float* nr = scalar_ptr(norm, "clip_factor");
-    const float* fin = factor_value.has_value() ? nullptr : scalar_ptr(factor, "clip_factor");
-    const float fval = factor_value.has_value() ? static_cast<float>(*factor_value) : 1.0f;
+    require_gpu(norm, "clip_factor");
     OnDevice on(norm);
-    check_rc(api().clip_factor(nr, fin, fval, scalar_ptr(grad_norm, "clip_factor"), scalar_ptr(factor, "clip_factor"),
-                               static_cast<float>(max_norm), on.stream), "z1_clip_factor");
+    const int dev = norm.device().index();
+    float* nr = scalar_ptr(norm, "clip_factor", dev);
+    const float* fin = factor_value.has_value() ? nullptr : scalar_ptr(factor, "clip_factor", dev);
+    const float fval = factor_value.has_value() ? static_cast<float>(*factor_value) : 1.0f;
+    check_rc(api().clip_factor(nr, fin, fval, scalar_ptr(grad_norm, "clip_factor", dev),
+                               scalar_ptr(factor, "clip_factor", dev), static_cast<float>(max_norm), on.stream),
+             "z1_clip_factor");
 }
 
 // ------------------------------------------------------------------------------------------ Adam + BF16
@@ -360,9 +375,9 @@ void adam_cast_impl(int64_t table, TensorList g, TensorList p, TensorList m, Ten
                     TensorList g32, const OptTensor& factor, double lr, double beta1, double beta2, double eps,
                     double bc1, double bc2, double weight_decay, int64_t adam_mode, int64_t row_begin,
                     int64_t row_end) {
-    float* fac = scalar_ptr(factor, "adam_cast");
     OnTable on(table);
     TableState& t = on.t;
+    float* fac = scalar_ptr(factor, "adam_cast", t.device);
     TORCH_CHECK(t.has_pmv, "yoco_z1: adam_cast needs a table with p, m and v");
     const int64_t nr = static_cast<int64_t>(t.sizes.size());
     TORCH_CHECK(0 <= row_begin && row_begin <= row_end && row_end <= nr, "yoco_z1: rows [", row_begin, ", ", row_end,
@@ -401,12 +416,12 @@ void adam_cast_gout_(int64_t table, TensorList g, TensorList p, TensorList m, Te
 void adam_cast_dev_(int64_t table, TensorList g, TensorList p, TensorList m, TensorList v, TensorList p16,
                     const OptTensor& factor, const Tensor& bc, double lr, double beta1, double beta2, double eps,
                     double weight_decay, int64_t adam_mode) {
-    float* fac = scalar_ptr(factor, "adam_cast_dev");
-    require_gpu(bc, "adam_cast_dev");
-    TORCH_CHECK(bc.scalar_type() == at::kFloat && bc.numel() >= 2 && bc.is_contiguous(),
-                "yoco_z1: bias corrections must be a contiguous 2-element fp32 tensor");
     OnTable on(table);
     TableState& t = on.t;
+    float* fac = scalar_ptr(factor, "adam_cast_dev", t.device);
+    require_on(bc, t.device, "adam_cast_dev");
+    TORCH_CHECK(bc.scalar_type() == at::kFloat && bc.numel() >= 2 && bc.is_contiguous(),
+                "yoco_z1: bias corrections must be a contiguous 2-element fp32 tensor");
     TORCH_CHECK(t.has_pmv, "yoco_z1: adam_cast_dev needs a table with p, m and v");
     const TensorList rest[4] = {p, m, v, p16};
     const TensorList none;
@@ -464,7 +479,7 @@ void owner_sum_(TensorList contribs, const Tensor& out, double scale, const OptT
     const int world = contributions(contribs, out, out_sum, ptrs);
     double* part = nullptr;
     if (partials.has_value() && partials->defined())
-        part = partials_ptr(*partials, "owner_sum", api().owner_sum_workspace(out.numel()));
+        part = partials_ptr(*partials, "owner_sum", out.device().index(), api().owner_sum_workspace(out.numel()));
     OnDevice on(out);
     check_rc(api().owner_sum_bf16(ptrs, world, out.numel(), static_cast<float>(scale),
                                   static_cast<uint16_t*>(out.data_ptr()), static_cast<float*>(ptr(out_sum)), part,
@@ -478,8 +493,9 @@ void owner_sum_update_(TensorList contribs, const Tensor& out, const Tensor& wor
                        std::optional<double> factor_value) {
     const uint16_t* ptrs[Z1_MAX_WORLD];
     const int world = contributions(contribs, out, out_sum, ptrs);
-    double* ws = partials_ptr(workspace, "owner_sum", api().owner_sum_workspace(out.numel()));
-    z1_update_scalars u = scalars("owner_sum_update", factor, factor_value, norm, grad_norm, flags, clip_log,
+    const int dev = out.device().index();
+    double* ws = partials_ptr(workspace, "owner_sum", dev, api().owner_sum_workspace(out.numel()));
+    z1_update_scalars u = scalars("owner_sum_update", dev, factor, factor_value, norm, grad_norm, flags, clip_log,
                                   sample_size, numer, max_norm);
     OnDevice on(out);
     check_rc(api().owner_sum_update(ptrs, world, out.numel(), static_cast<float>(scale),
@@ -496,6 +512,7 @@ void sum_slots_(const Tensor& staging, const Tensor& out, int64_t G, int64_t bas
                 staging.is_contiguous(), "ce_reduce: staging must be a contiguous bf16 GPU tensor");
     TORCH_CHECK(out.defined() && out.is_cuda() && out.scalar_type() == at::kBFloat16 && out.is_contiguous(),
                 "ce_reduce: out must be a contiguous bf16 GPU tensor");
+    TORCH_CHECK(staging.device() == out.device(), "ce_reduce: staging and out must be on one device");
     TORCH_CHECK(1 <= world && world <= Z1_MAX_WORLD && 0 <= rank && rank < world, "ce_reduce: rank ", rank,
                 " / world ", world, " out of range");
     TORCH_CHECK(0 <= base && base <= end && end <= G && out.numel() >= G && staging.numel() >= (world - 1) * G,
@@ -519,6 +536,8 @@ void scale_up_(const Tensor& g16, const Tensor& g32, const Tensor& factor) {
     require_gpu(factor, "scale_up");
     TORCH_CHECK(g16.scalar_type() == at::kBFloat16 && g32.scalar_type() == at::kFloat && g16.numel() == g32.numel(),
                 "yoco_z1: scale_up expects bf16 -> fp32 of equal size");
+    TORCH_CHECK(g16.device() == g32.device() && factor.device() == g32.device(),
+                "yoco_z1: scale_up's tensors must be on one device");
     TORCH_CHECK(g16.is_contiguous() && g32.is_contiguous(), "yoco_z1: scale_up expects contiguous tensors");
     TORCH_CHECK(factor.scalar_type() == at::kFloat && factor.numel() >= 1,
                 "scale_up: expected a 1-element fp32 device tensor");
@@ -532,6 +551,7 @@ void cast_bf16_(const Tensor& p32, const Tensor& p16) {
     require_gpu(p16, "cast_bf16");
     TORCH_CHECK(p32.scalar_type() == at::kFloat && p16.scalar_type() == at::kBFloat16 && p32.numel() == p16.numel(),
                 "yoco_z1: cast_bf16 expects fp32 -> bf16 of equal size");
+    TORCH_CHECK(p32.device() == p16.device(), "yoco_z1: cast_bf16's tensors must be on one device");
     TORCH_CHECK(p32.is_contiguous() && p16.is_contiguous(), "yoco_z1: cast_bf16 expects contiguous tensors");
     OnDevice on(p32);
     check_rc(api().cast_bf16(static_cast<const float*>(p32.data_ptr()), static_cast<uint16_t*>(p16.data_ptr()),

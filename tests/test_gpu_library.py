@@ -119,3 +119,46 @@ def test_profiler_sees_the_operators(pkg, dev):
         torch.cuda.synchronize()
     names = {e.name for e in prof.events()}
     assert {'yoco_z1::grad_norm_clip_', 'yoco_z1::adam_cast_'} <= names, sorted(n for n in names if 'yoco' in n)
+
+
+def test_operators_refuse_tensors_off_the_launch_device(pkg, dev):
+    """Every auxiliary tensor of a launch (norm workspace, factor and scalar outputs, flags, bias corrections,
+    owner-sum workspace, staging, scale/cast operands) must live on the launch's device: each operator raises
+    before enqueuing anything, and the state it would have written is untouched.  With one GPU the other device is
+    the host; the same check compares device indices between GPUs."""
+    from faster_yoco_amd import ops
+    Y = torch.ops.yoco_z1
+    n = 3000
+    gen = torch.Generator(device='cpu').manual_seed(11)
+    g = (torch.randn(n, generator=gen) * 1e-2).to(dev)
+    p, m = (torch.randn(n, generator=gen) * 0.02).to(dev), (torch.randn(n, generator=gen) * 1e-4).to(dev)
+    v, p16 = (torch.randn(n, generator=gen) * 1e-8).abs().to(dev), torch.zeros(n, dtype=torch.bfloat16, device=dev)
+    table = ops.Table([(g, p, m, v, p16, n)], dev)
+    t = table.handle_int
+    part = ops.norm_workspace(dev)
+    one = lambda: torch.zeros(1, device=dev)
+    host1 = lambda: torch.zeros(1)
+    before = [x.clone() for x in (p, m, v, p16)]
+    calls = [
+        lambda: Y.grad_sumsq_(t, [g], part.cpu()),
+        lambda: Y.grad_norm_clip_(t, [g], part, host1(), one(), one(), 1.0, 0.5),
+        lambda: Y.norm_clip_(part, one(), host1(), one(), 1.0, None),
+        lambda: Y.update_scalars_(part, one(), one(), one(), torch.zeros(2, dtype=torch.uint8), None, None, 1.0,
+                                  1.0, None),
+        lambda: Y.grad_update_scalars_(t, [g], part, one(), one(), one(), None, host1(), None, 1.0, 1.0, None),
+        lambda: Y.clip_factor_(torch.tensor([3.0], device=dev), host1(), one(), 1.0, None),
+        lambda: Y.adam_cast_(t, [g], [p], [m], [v], [p16], host1(), 3e-4, 0.9, 0.95, 1e-8, 0.1, 0.05, 0.1, 1, 0, 1),
+        lambda: Y.adam_cast_dev_(t, [g], [p], [m], [v], [p16], one(), torch.ones(2), 3e-4, 0.9, 0.95, 1e-8, 0.1, 1),
+        lambda: Y.owner_sum_([p16, p16.clone()], torch.empty_like(p16), 0.5, None, ops.norm_workspace(dev, n).cpu()),
+        lambda: Y.owner_sum_update_([p16, p16.clone()], torch.empty_like(p16), ops.norm_workspace(dev, n), 0.5, None,
+                                    host1(), None, None, None, None, None, 1.0, 1.0, None),
+        lambda: Y.sum_slots_(torch.zeros(n, dtype=torch.bfloat16), torch.empty_like(p16), n, 0, n, 0, 0.5, 2),
+        lambda: Y.scale_up_(p16, torch.empty(n, device=dev), torch.tensor([0.25])),
+        lambda: Y.cast_bf16_(p, torch.empty(n, dtype=torch.bfloat16)),
+    ]
+    for i, call in enumerate(calls):
+        with pytest.raises(RuntimeError):
+            call()
+        torch.cuda.synchronize()
+        for a, b in zip((p, m, v, p16), before):
+            assert torch.equal(a, b), f'call {i} changed the state before refusing'
