@@ -380,6 +380,33 @@ def test_owner_sum_bit_exact(pkg, dev, world):
     assert abs(float(nr.item()) - ex) <= 1e-6 * ex
 
 
+KEEP_ELEMS = (224 << 20) // 2         # the owner sum's second launch: the average's last 224 MB (kept in the MALL)
+
+
+@pytest.mark.parametrize('n', [KEEP_ELEMS - 300, KEEP_ELEMS, KEEP_ELEMS + 1, KEEP_ELEMS + 257])
+def test_owner_sum_around_the_mall_keep_split(pkg, dev, n):
+    """Sizes where the owner sum's first launch covers no chunk (all of the average fits the kept window, the last
+    chunk whole or partial) or only one or two: the average, the fp32 sum and the fused norm against the oracle."""
+    from faster_yoco_amd import ops
+    rng = np.random.default_rng(n)
+    world = 2
+    cs = [(rng.integers(0x3000, 0x4000, n, dtype=np.uint16) | (rng.integers(0, 2, n, dtype=np.uint16) << 15))
+          .astype(np.uint16) for _ in range(world)]
+    avg, s = oracle.owner_sum(cs, want_sum=True)
+    ts = [dev_bf16(c, dev) for c in cs]
+    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    osum = torch.empty(n, dtype=torch.float32, device=dev)
+    part = ops.norm_workspace(dev, n)
+    ops.owner_sum(ts, out, 1.0 / world, out_sum=osum, partials=part)
+    nr = torch.zeros(1, device=dev)
+    ops.norm_clip(part, norm_out=nr)
+    torch.cuda.synchronize()
+    assert same_bf16(host_bf16(out), avg)
+    assert same_f32(host_f32(osum), s)
+    ex = float(np.sqrt(oracle.sumsq(avg)))
+    assert abs(float(nr.item()) - ex) <= 1e-6 * ex
+
+
 def test_owner_sum_in_place_reference_slot_layout(pkg, dev):
     from faster_yoco_amd import ce_reduce
     rng = np.random.default_rng(9)

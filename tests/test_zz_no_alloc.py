@@ -1,7 +1,8 @@
 """z1_owner_sum_update_noalloc (the entry point that allocates nothing: its workspace is the library's static device
 scratch) against z1_owner_sum_update with a caller workspace, through the C ABI: two calls in a row, the second on a
 smaller input, every output bit-identical (the BF16 average, the FP32 sum, norm, grad_norm, factor, the two flags
-and the clip metric).  Sizes beyond Z1_NOALLOC_MAX_N are refused before any device work."""
+and the clip metric); the same at Z1_NOALLOC_MAX_N elements, where the whole scratch is in use.  Sizes beyond
+Z1_NOALLOC_MAX_N are refused before any device work."""
 import ctypes
 
 import numpy as np
@@ -57,6 +58,20 @@ def test_noalloc_owner_sum_update_matches_the_workspace_entry_point(pkg, dev):
         for k in want:
             assert np.array_equal(got[k], want[k]), (n, k)
         assert got['flags'].tolist() == [1, 1]
+
+
+def test_noalloc_at_its_maximum_size(pkg, dev):
+    """Z1_NOALLOC_MAX_N elements: every slot of the scratch in use (the norm's partials, then one per 256-element
+    chunk), the same bits as the workspace form."""
+    from faster_yoco_amd import _lib
+    n = _lib.Z1_NOALLOC_MAX_N
+    gen = torch.Generator(device=dev).manual_seed(5)
+    contribs = [(torch.randn(n, generator=gen, device=dev) * 1e-2).to(torch.bfloat16) for _ in range(2)]
+    want = _call(pkg, dev, contribs, n, noalloc=False)
+    got = _call(pkg, dev, contribs, n, noalloc=True)
+    for k in want:
+        assert np.array_equal(got[k], want[k]), k
+    assert got['flags'].tolist() == [1, 1]
 
 
 def test_noalloc_refuses_sizes_beyond_its_scratch(pkg, dev):
