@@ -110,6 +110,7 @@ class FusedAdamCast:
 
 
 def scale_up(g16, g32, factor):
-    """g32 = float(g16) * factor (factor: 1-element fp32 tensor) -- the fp32 product of the exactly upcast value, as
-    torch.mul(g16, factor, out=g32) computes it."""
+    """Scale pass of yoco/tasks/fused_adam_cast.py:84-89: each BF16 gradient element is widened to fp32 (exact) and
+    multiplied by the device scalar ``factor`` (one fp32 element) with one fp32 rounding, written to ``g32``; the
+    bits torch's ``mul`` of a bf16 tensor by an fp32 scalar tensor into an fp32 output gives."""
     ops.scale_up(g16, g32, factor)
