@@ -9,7 +9,10 @@ Prints ONE JSON line: ms per step (the metric), the Adam kernel's roofline from 
 launch stream, and the PyTorch-CPU restatement's time on a bounded sample of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--config c2] [--cpu-sample-tensors T] [--no-cpu-baseline] [--dropin]
-                    [--pipeline K]
+                    [--pipeline K] [--no-dropin-step] [--no-side]
+
+With c2 or c3 the line also carries ``dropin_step``: the update at C3's shape through the reference's own seams
+(CEReduce._sum per phase, zero1_fast.clip_grad_norm, zero1_fast.step -> FusedAdamCast), timed after the main steps.
 """
 import argparse
 import json
@@ -210,6 +213,157 @@ def dropin_timing(dev, hp, step, reps=10):
     return out
 
 
+def dropin_step_timing(dev, hp, step0, steps=20, warmup=5, world=8, rank=3):
+    """One update through the reference's own seams at C3's shape, as its trainer runs it with the measured switches
+    of scripts/configs/faster.env (ZERO1_FAST, ALLGATHER, PARAM_VIEWS, PARAM_ALLREDUCE + GRAD_REDUCE_OWNER,
+    Z1_ONE_PASS, Z1_SCALE_KERNEL, FUSED_ADAM, CE_REDUCE):
+      1. CEReduce._sum per phase (this build's, installed on a CEReduce with the reference's slot-major staging:
+         8 BF16 contributions of the owner's 430,662,912-element gradient, rank 3's own in ``out``, laid out by
+         backward phase as the reference lays it out; phases 0-1 on a side stream and then the last on the
+         current one, as CEReduce.push / finish run them, yoco/models/decoder/ce_reduce.py:205-209,227-228), then
+         the owned gradients made views of ``out`` (:232-237);
+      2. zero1_fast.clip_grad_norm(1.0) (yoco/tasks/zero1_fast.py:139-162);
+      3. zero1_fast.step() (:165-235) -> OSS.step -> FusedAdamV2.step -> FusedAdamCast: BF16 gradients folded in
+         with the factor, FP32 master gradients written by the same launch;
+    over the 38 C3 tensors, with fairseq's per-parameter FP32 masters, gradients and moments, and the BF16
+    parameters placed in one flat buffer (fairseq / fairscale stand-ins, faster_yoco_amd.standins).
+    Algorithmic bytes: owner sum 18 B/param (8 x 2 in, 2 out) + Adam 32 B/param (BF16 g 2, p / m / v 12 in; p / m / v
+    12, BF16 copy 2, FP32 gradient 4 out); the norm reads nothing (the phase sums left its partials).  Timed
+    steps chain: rank 3's own slot then holds the previous step's average, the same bytes and launches.  Also timed:
+    the same with the norm read again from the gradients (ce_reduce.FUSE_NORM off, +2 B/param), and the phase sums
+    alone with phase bounds on parameter boundaries and with bounds moved off every alignment."""
+    import torch
+    from faster_yoco_amd import ce_reduce, configs, layout, standins, zero1_fast
+    shapes = configs.shapes('c3')
+    numels = [math.prod(sh) for sh in shapes]
+    G = sum(numels)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(3)
+
+    def normal(n, std, dtype=torch.float32):
+        return (torch.randn(n, generator=gen, device=dev) * std).to(dtype)
+
+    params = [torch.nn.Parameter(normal(n, 0.02, torch.bfloat16).view(sh)) for n, sh in zip(numels, shapes)]
+    saved = {k: getattr(zero1_fast, k) for k in zero1_fast._SWITCHES}
+    saved_orig, saved_placed = dict(zero1_fast._ORIG), dict(zero1_fast._PLACED)
+    zero1_fast.configure(ENABLED=True, ALLGATHER=True, PARAM_VIEWS=True, REDUCE_OWNER=True, ONE_PASS=True,
+                         SCALE_KERNEL=True, FUSED_ADAM=True, CE_ALLGATHER=False, FOLD_SCALE=False)
+    zero1_fast._PLACED.clear()
+    zero1_fast._PLACED.update(layout.place_params(params, 1))
+
+    class Mixin(standins.FakeMixin):
+        pass
+
+    class Opt(Mixin, standins.FakeFP16Optimizer):
+        pass
+
+    zero1_fast._ORIG.clear()
+    zero1_fast.install(Mixin)
+    opt = Opt(params, lr=hp['lr'], betas=hp['betas'], eps=hp['eps'], weight_decay=hp['weight_decay'])
+    adam = opt.fp32_optimizer.optimizer.optim
+    adam.param_groups[0]['step'] = step0 - 1
+    for p32, n in zip(opt.fp32_params, numels):
+        adam.state[p32] = {'exp_avg': normal(n, 1e-4).view_as(p32),
+                           'exp_avg_sq': normal(n, 1e-8).abs_().view_as(p32)}
+    staging = normal((world - 1) * G, 1e-4, torch.bfloat16)
+    out = normal(G, 1e-4, torch.bfloat16)
+    # CEReduce's layout (ce_reduce.py:122-140): the owner's gradients ordered by backward phase, then model order;
+    # three phases as layer_graphs.py:207-221 assigns them -- 0: the model's last parameters (output projection,
+    # final norm, cross decoder), 1: the middle, 2: the first ones -- here the last, middle and first 12-13 tensors
+    phase_of = [2] * 13 + [1] * 13 + [0] * (len(shapes) - 26)
+    order = sorted(range(len(shapes)), key=lambda i: (phase_of[i], i))
+    where, bounds, off = {}, [[0, 0] for _ in range(3)], 0
+    for i in order:
+        ph = phase_of[i]
+        if bounds[ph][1] == 0:
+            bounds[ph] = [off, off]
+        where[i] = off
+        off += numels[i]
+        bounds[ph][1] = off
+    cls = ce_reduce.install(type('CEReduce', (standins.FakeCEReduce,), {}))
+    ce = cls(staging, out, G, bounds, rank, world)
+    views = [out[where[i]:where[i] + n].view(sh) for i, (n, sh) in enumerate(zip(numels, shapes))]
+    side = torch.cuda.Stream(device=dev)
+
+    def sums():
+        # phases 0 .. n-2 on the side stream, as CEReduce.push launches them during the backward; the last one on
+        # the current stream, as finish() does, after them (in the reference the rest of the backward separates
+        # them; launched side by side, two owner sums contend and take 1.22 instead of 1.18 ms)
+        cur = torch.cuda.current_stream(dev)
+        side.wait_stream(cur)
+        with torch.cuda.stream(side):
+            for ph in range(len(ce.bounds) - 1):
+                ce._sum(ph)
+        cur.wait_stream(side)
+        ce._sum(len(ce.bounds) - 1)
+
+    def update(ev=None):
+        if ev is not None:
+            ev[0].record()
+        sums()
+        for p, g in zip(params, views):
+            p.grad = g
+        if ev is not None:
+            ev[1].record()
+        opt.clip_grad_norm(hp['max_norm'])
+        if ev is not None:
+            ev[2].record()
+        opt.step()
+        if ev is not None:
+            ev[3].record()
+        opt.zero_grad()
+
+    def timed(fn, k):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        t0 = time.perf_counter()
+        for _ in range(k):
+            fn()
+        host = time.perf_counter() - t0
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / k, host / k
+
+    res = {'tensors': len(shapes), 'params': G, 'world': world, 'rank': rank, 'phases': len(ce.bounds)}
+    try:
+        for _ in range(warmup):
+            update()
+        ms, host = timed(update, steps)
+        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(5)]
+        for e in ev:
+            update(e)
+        torch.cuda.synchronize()
+        med = lambda xs: sorted(xs)[len(xs) // 2]
+        stage = {'sums_ms': med([e[0].elapsed_time(e[1]) for e in ev]),
+                 'clip_ms': med([e[1].elapsed_time(e[2]) for e in ev]),
+                 'adam_ms': med([e[2].elapsed_time(e[3]) for e in ev])}
+        nbytes = 50 * G
+        res.update({'ms': round(ms, 4), 'host_us': round(host * 1e6, 1), 'algorithmic_bytes': nbytes,
+                    'achieved_GBps': round(nbytes / (ms * 1e-3) / 1e9, 1),
+                    'frac_of_peak': round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+                    'stage_ms': {k: round(v, 4) for k, v in stage.items()}})
+        ce_reduce.FUSE_NORM = False
+        for _ in range(2):
+            update()
+        ms_u, _ = timed(update, steps)
+        res['norm_read_again_ms'] = round(ms_u, 4)
+        ce_reduce.FUSE_NORM = True
+        res['sums_aligned_bounds_ms'] = round(timed(sums, steps)[0], 4)
+        odd = [0, bounds[0][1] + 1, bounds[1][1] + 3, G]        # 2- and 6-byte offsets: no common alignment
+        ce.bounds = [[odd[i], odd[i + 1]] for i in range(3)]
+        sums()
+        res['sums_odd_bounds_ms'] = round(timed(sums, steps)[0], 4)
+    finally:
+        ce_reduce.FUSE_NORM = True
+        zero1_fast.configure(**saved)
+        zero1_fast._ORIG.clear()
+        zero1_fast._ORIG.update(saved_orig)
+        zero1_fast._PLACED.clear()
+        zero1_fast._PLACED.update(saved_placed)
+    return res
+
+
 def pipeline_timing(shard, opt, k, reps=10):
     """Adam in k row ranges of the shard with each finished range's BF16 rows copied out on a second stream
     (faster_yoco_amd.exchange: the exchange the reference runs after the whole step, yoco/tasks/zero1_fast.py:224-226,
@@ -305,6 +459,10 @@ def main():
     ap.add_argument('--dropin', action='store_true',
                     help='also time FusedAdamCast over the 38 C2 tensors allocated one by one (its launches share '
                          'the Adam kernel with the timed steps, so a kernel trace of the default run stays clean)')
+    ap.add_argument('--no-dropin-step', action='store_true',
+                    help='skip the update through the reference\'s own seams at C3\'s shape (dropin_step)')
+    ap.add_argument('--dropin-step-only', action='store_true',
+                    help='only time dropin_step (--steps / --warmup apply to it), e.g. for counter runs')
     ap.add_argument('--no-side', action='store_true',
                     help='skip the side measurements (trainer scalar chain, embedding gradient), e.g. for counter runs')
     ap.add_argument('--calibrate-copy', action='store_true',
@@ -332,6 +490,10 @@ def main():
 
     dev = torch.device('cuda:0')
     torch.cuda.set_device(dev)
+    if args.dropin_step_only:
+        print(json.dumps({'dropin_step': dropin_step_timing(dev, configs.HPARAMS, configs.CONFIGS['c3']['step'],
+                                                            steps=args.steps, warmup=args.warmup)}), flush=True)
+        return
     cfg = args.config
     hp = configs.HPARAMS
     gdt = torch.bfloat16 if cfg == 'c3' else torch.float32
@@ -427,6 +589,10 @@ def main():
         out['dropin_multi_tensor_adam'] = dropin_timing(dev, hp, step0)
     if args.pipeline > 0:
         out['pipelined_exchange'] = pipeline_timing(shard, opt, args.pipeline)
+    if not args.no_dropin_step and cfg in ('c2', 'c3'):
+        del shard, opt, contribs                       # the shard's 15 GB, before the drop-in's own state
+        torch.cuda.empty_cache()
+        out['dropin_step'] = dropin_step_timing(dev, hp, configs.CONFIGS['c3']['step'])
     print(json.dumps(out), flush=True)
 
 

@@ -15,8 +15,10 @@ Modules
     trainer_glue     the optimizer part of trainer_nosync.train_step: one-launch scalar chain + deferred checks
     exchange         the BF16 exchange pipelined with the step (row ranges, side-stream sends)
     configs          the benchmark/parity workloads (tensor lists and synthetic inputs)
+    standins         stand-ins of the fairseq / fairscale objects the drop-in surfaces are driven through where
+                     those packages are absent (tests, bench.py); never used by the product path
 """
 from . import _lib, library, ops  # noqa: F401
 
 __all__ = ['library', 'ops', 'kernels', 'shard', 'fused_adam_cast', 'zero1_fast', 'ce_reduce', 'configs', 'layout',
-           'trainer_glue', 'embedding', 'exchange']
+           'trainer_glue', 'embedding', 'exchange', 'standins']

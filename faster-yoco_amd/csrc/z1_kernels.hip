@@ -518,19 +518,29 @@ struct Srcs {
 // write request of its own: 54 MB of 32-byte requests at C3's size).
 constexpr int kSumVec = 4;                                    // elements per lane and chunk
 constexpr int64_t kSumChunk = (int64_t)kWave * kSumVec;
+// The chunk grid is shifted by `shift` elements (0..kSumShiftMax): chunk c covers elements [c * kSumChunk - shift,
+// (c + 1) * kSumChunk - shift) of the call's range.  The host picks the shift that puts the chunk boundaries on
+// 128-byte lines of every stream (else on their 8-byte words), so a range that starts anywhere -- a CEReduce phase
+// bound, yoco/models/decoder/ce_reduce.py:178-183 -- keeps the vector path, and no line is shared by two chunks
+// (consecutive chunks run on different XCDs, whose L2s would each fetch a shared line).  A call always launches
+// owner_sum_waves(n) chunks, enough for any shift; those past the end only write a zero partial.
+constexpr int64_t kSumShiftMax = 63;
+
+__device__ __host__ constexpr int64_t owner_sum_waves(int64_t n) {
+    return n <= 0 ? 0 : (n + kSumShiftMax + kSumChunk - 1) / kSumChunk;
+}
 
 template <int W, bool KEEP>
 __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, float scale, uint16_t* out,
                                                           float* out_sum, double* wave_partials, int vec,
-                                                          int64_t chunk_base) {
+                                                          int64_t chunk_base, int64_t shift) {
     const int64_t c = chunk_base + (int64_t)blockIdx.x;
-    const int64_t e0 = c * kSumChunk + (int64_t)threadIdx.x * kSumVec;
+    const int64_t e0 = c * kSumChunk + (int64_t)threadIdx.x * kSumVec - shift;
     double acc2 = 0.0;
-    if (vec && e0 + kSumVec <= n) {
-        const int64_t gi = e0 / kSumVec;
+    if (vec && e0 >= 0 && e0 + kSumVec <= n) {
         u2 x[W];
 #pragma unroll
-        for (int k = 0; k < W; ++k) x[k] = ld(reinterpret_cast<const u2*>(s.p[k]) + gi);
+        for (int k = 0; k < W; ++k) x[k] = ld(reinterpret_cast<const u2*>(s.p[k] + e0));
         float a[kSumVec];
 #pragma unroll
         for (int j = 0; j < kSumVec; ++j) a[j] = 0.0f;
@@ -545,9 +555,9 @@ __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, flo
         u2 o;
 #pragma unroll
         for (int w = 0; w < kSumVec / 2; ++w) o[w] = pack_bf16(a[2 * w] * scale, a[2 * w + 1] * scale);
-        if (KEEP) st_keep(reinterpret_cast<u2*>(out) + gi, o);
-        else st(reinterpret_cast<u2*>(out) + gi, o);
-        if (out_sum) st(reinterpret_cast<f4*>(out_sum) + gi, f4{a[0], a[1], a[2], a[3]});
+        if (KEEP) st_keep(reinterpret_cast<u2*>(out + e0), o);
+        else st(reinterpret_cast<u2*>(out + e0), o);
+        if (out_sum) st(reinterpret_cast<f4*>(out_sum + e0), f4{a[0], a[1], a[2], a[3]});
         if (wave_partials) {
 #pragma unroll
             for (int w = 0; w < kSumVec / 2; ++w) {
@@ -556,8 +566,9 @@ __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, flo
             }
         }
     } else {
+        const int64_t b = e0 > 0 ? e0 : 0;
         const int64_t e1 = e0 + kSumVec < n ? e0 + kSumVec : n;
-        for (int64_t e = e0; e < e1; ++e) {
+        for (int64_t e = b; e < e1; ++e) {
             float a = 0.0f;
 #pragma unroll
             for (int k = 0; k < W; ++k) a = a + bf16_to_f32(s.p[k][e]);
@@ -593,16 +604,18 @@ __global__ __launch_bounds__(kThreads) void reduce_partials_kernel(const double*
 // kernel the compiler merges the two kinds of store into one ordinary store.
 template <int W>
 void launch_owner_sum(int world, int64_t nchunks, int64_t keep_from, size_t lds, hipStream_t st, const Srcs& s,
-                      int64_t n, float scale, uint16_t* out, float* out_sum, double* wave_partials, int vec) {
+                      int64_t n, float scale, uint16_t* out, float* out_sum, double* wave_partials, int vec,
+                      int64_t shift) {
     if (world == W) {
         if (keep_from > 0)
             hipLaunchKernelGGL((owner_sum_kernel<W, false>), dim3((unsigned)keep_from), dim3(kWave), lds, st, s,
-                               n, scale, out, out_sum, wave_partials, vec, (int64_t)0);
+                               n, scale, out, out_sum, wave_partials, vec, (int64_t)0, shift);
         if (nchunks > keep_from)
             hipLaunchKernelGGL((owner_sum_kernel<W, true>), dim3((unsigned)(nchunks - keep_from)), dim3(kWave),
-                               lds, st, s, n, scale, out, out_sum, wave_partials, vec, keep_from);
+                               lds, st, s, n, scale, out, out_sum, wave_partials, vec, keep_from, shift);
     } else if constexpr (W > 1) {
-        launch_owner_sum<W - 1>(world, nchunks, keep_from, lds, st, s, n, scale, out, out_sum, wave_partials, vec);
+        launch_owner_sum<W - 1>(world, nchunks, keep_from, lds, st, s, n, scale, out, out_sum, wave_partials, vec,
+                                shift);
     }
 }
 
@@ -756,8 +769,7 @@ inline int launch_status() {
 // owner-sum chunk, for up to Z1_NOALLOC_MAX_N elements (16.0 MiB; every device the library runs on holds its own copy
 // until the process ends).  Host code never passes this name to a kernel: in host code it is a stand-in, not a
 // device address.  The address of a device's copy comes from hipGetSymbolAddress, once per device.
-constexpr int64_t kNoallocDoubles = Z1_NORM_PARTIALS + Z1_NOALLOC_MAX_N / kSumChunk;
-static_assert(Z1_NOALLOC_MAX_N % kSumChunk == 0, "the no-allocation maximum is a whole number of chunks");
+constexpr int64_t kNoallocDoubles = Z1_NORM_PARTIALS + owner_sum_waves(Z1_NOALLOC_MAX_N);
 static __device__ __align__(256) double scratch[kNoallocDoubles];
 
 namespace {
@@ -795,6 +807,8 @@ struct z1_table {
     int64_t nchunks;
     std::vector<Row> host_rows;   // host copy of the device rows' pointers, kept by rebind / set_grads
     int host_valid;       // 0 once a rebind / set_grads launch failed: the device rows may differ from host_rows
+    int rows_failed;      // a rebind / set_grads launch failed: launches are refused until a z1_table_rebind succeeds
+    int gout_failed;      // a set_grad_out launch failed: Adam is refused until a z1_table_set_grad_out succeeds
     int contig;           // the device rows tile one allocation per stream in order, without gaps (see set_contig)
     Row whole;            // when contig: the first row's pointers, n = numel, the vector flags of the whole
 };
@@ -998,6 +1012,7 @@ int z1_table_rebind(z1_table* table, const z1_tensor* rows, int nrows, void* str
             rc = launch_status();
             if (rc) {
                 table->host_valid = 0;
+                table->rows_failed = 1;
                 return rc;
             }
             b.count = 0;
@@ -1008,9 +1023,12 @@ int z1_table_rebind(z1_table* table, const z1_tensor* rows, int nrows, void* str
         rc = launch_status();
         if (rc) {
             table->host_valid = 0;
+            table->rows_failed = 1;
             return rc;
         }
     }
+    table->host_valid = 1;                             // every row's pointers as host_rows now holds them
+    table->rows_failed = 0;
     set_contig(table);
     return Z1_OK;
 }
@@ -1041,6 +1059,7 @@ int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* s
             rc = launch_status();
             if (rc) {
                 table->host_valid = 0;
+                table->rows_failed = 1;
                 return rc;
             }
             b.count = 0;
@@ -1051,6 +1070,7 @@ int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* s
         rc = launch_status();
         if (rc) {
             table->host_valid = 0;
+            table->rows_failed = 1;
             return rc;
         }
     }
@@ -1078,16 +1098,23 @@ int z1_table_set_grad_out(z1_table* table, float* const* g32, int nrows, void* s
         if (++b.count == kBindPerLaunch) {
             hipLaunchKernelGGL(set_grad_out_kernel, dim3(1), dim3(kBindPerLaunch), 0, s, table->gout, b);
             rc = launch_status();
-            if (rc) return rc;
+            if (rc) {
+                table->gout_failed = 1;            // the column may be half rewritten
+                return rc;
+            }
             b.count = 0;
         }
     }
     if (b.count) {
         hipLaunchKernelGGL(set_grad_out_kernel, dim3(1), dim3(kBindPerLaunch), 0, s, table->gout, b);
         rc = launch_status();
-        if (rc) return rc;
+        if (rc) {
+            table->gout_failed = 1;
+            return rc;
+        }
     }
     table->gout_rows = set;
+    table->gout_failed = 0;
     return Z1_OK;
 }
 
@@ -1106,6 +1133,7 @@ static int launch_sumsq(const z1_table* table, double* partials, const z1_update
     int dev = 0;
     int rc = check_table_device(table, &dev);
     if (rc) return rc;
+    if (table->rows_failed) return Z1_E_STATE;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t kf = keep_from(table);
     if (table->g_dtype == Z1_F32)
@@ -1182,6 +1210,7 @@ static int adam_launch(const z1_table* table, int64_t chunk_begin, int64_t chunk
     int dev = 0;
     int rc = check_table_device(table, &dev);
     if (rc) return rc;
+    if (table->rows_failed || table->gout_failed) return Z1_E_STATE;
     if (chunk_end <= chunk_begin) return Z1_OK;
     AdamK k;
     k.lr = lr;
@@ -1265,34 +1294,63 @@ int z1_bias_corrections_step(int64_t* step, double beta1, double beta2, int bias
     return launch_status();
 }
 
-int64_t z1_owner_sum_workspace(int64_t n) {
+int64_t z1_owner_sum_waves(int64_t n) {
     if (n < 0) return Z1_E_SIZE;
-    return Z1_NORM_PARTIALS + n / kSumChunk + (n % kSumChunk != 0);   // the partials, then one per chunk
+    return owner_sum_waves(n);
 }
 
-// The owner sum with the fused norm when a workspace is given: the per-wave partials' fixed-order reduction leaves
-// the Z1_NORM_PARTIALS partials in the workspace (z1_owner_sum_bf16), and with a tail the one-workgroup final
-// reduction + scalar chain follows (z1_owner_sum_update).
+int64_t z1_owner_sum_workspace(int64_t n) {
+    if (n < 0) return Z1_E_SIZE;
+    return Z1_NORM_PARTIALS + owner_sum_waves(n);   // the partials, then one per chunk
+}
+
+// Shift of the owner sum's chunk grid (owner_sum_kernel) for these streams, and whether the vector path applies:
+// when every bf16 stream lies at the same offset within a 128-byte line as out_avg, the chunk boundaries go on those
+// lines; else, when they share the offset within an 8-byte word, on the words; else the element-wise path.  The
+// FP32 sum (nullable) must then be 16-byte aligned at the same boundaries.
+static int owner_sum_grid(const Srcs& s, int world, const uint16_t* out_avg, const float* out_sum, int64_t* shift) {
+    const uintptr_t o = reinterpret_cast<uintptr_t>(out_avg);
+    *shift = 0;
+    if (o & 1) return 0;
+    uintptr_t diff = 0;
+    for (int k = 0; k < world; ++k) diff |= reinterpret_cast<uintptr_t>(s.p[k]) - o;
+    int64_t sh;
+    if ((diff & 127) == 0) sh = (int64_t)((o & 127) >> 1);
+    else if ((diff & 7) == 0) sh = (int64_t)((o & 7) >> 1);
+    else return 0;
+    if (out_sum) {
+        const uintptr_t f = reinterpret_cast<uintptr_t>(out_sum);
+        if ((f & 3) || (((f >> 2) - (uintptr_t)sh) & 3)) return 0;
+    }
+    *shift = sh;
+    return 1;
+}
+
+// The owner sum; with `waves` (owner_sum_waves(n) doubles) each chunk's FP64 norm partial is written there, and with
+// a workspace (z1_owner_sum_workspace(n) doubles: the Z1_NORM_PARTIALS partials, then the per-chunk ones) the
+// per-chunk partials' fixed-order reduction leaves the Z1_NORM_PARTIALS partials at its start (z1_owner_sum_bf16),
+// followed, with a tail, by the one-workgroup final reduction + scalar chain (z1_owner_sum_update).
 static int owner_sum(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
-                     float* out_sum, double* workspace, const z1_update_scalars* tail, void* stream) {
+                     float* out_sum, double* waves, double* workspace, const z1_update_scalars* tail, void* stream,
+                     bool keep_end = true) {
     if (!contrib) return Z1_E_NULL;
     if (world < 1 || world > Z1_MAX_WORLD) return Z1_E_WORLD;
     if (n < 0) return Z1_E_SIZE;
     if (n > 0 && !out_avg) return Z1_E_NULL;               // empty inputs may carry NULL data pointers
     Srcs srcs;
     memset(&srcs, 0, sizeof(srcs));
-    int vec = aligned(out_avg, 16) && (!out_sum || aligned(out_sum, 16));
     for (int k = 0; k < world; ++k) {
         if (n > 0 && !contrib[k]) return Z1_E_NULL;
         srcs.p[k] = contrib[k];
-        if (!aligned(contrib[k], 16)) vec = 0;
     }
-    const int64_t nchunks = n / kSumChunk + (n % kSumChunk != 0);
+    int64_t shift = 0;
+    const int vec = owner_sum_grid(srcs, world, out_avg, out_sum, &shift);
+    const int64_t nchunks = owner_sum_waves(n);
     if (nchunks > INT32_MAX) return Z1_E_SIZE;
     hipStream_t st = static_cast<hipStream_t>(stream);
-    double* wave_partials = workspace ? workspace + Z1_NORM_PARTIALS : nullptr;
+    double* wave_partials = workspace ? workspace + Z1_NORM_PARTIALS : waves;
     if (nchunks > 0) {
-        const int64_t keep = kOwnerSumKeepBytes / (kSumChunk * (int64_t)sizeof(uint16_t));
+        const int64_t keep = keep_end ? kOwnerSumKeepBytes / (kSumChunk * (int64_t)sizeof(uint16_t)) : 0;
         const int64_t keep_from = nchunks > keep ? nchunks - keep : 0;
         int dev = 0;
         size_t lds = 0;
@@ -1300,7 +1358,7 @@ static int owner_sum(const uint16_t* const* contrib, int world, int64_t n, float
         if (rc == Z1_OK) rc = occupancy_lds(dev, kOwnerSumWgPerCu, &lds);
         if (rc) return rc;
         launch_owner_sum<Z1_MAX_WORLD>(world, nchunks, keep_from, lds, st, srcs, n, scale, out_avg, out_sum,
-                                       wave_partials, vec);
+                                       wave_partials, vec, shift);
         rc = launch_status();
         if (rc) return rc;
     }
@@ -1315,13 +1373,27 @@ static int owner_sum(const uint16_t* const* contrib, int world, int64_t n, float
 
 int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
                       float* out_sum, double* sumsq_partials, void* stream) {
-    return owner_sum(contrib, world, n, scale, out_avg, out_sum, sumsq_partials, nullptr, stream);
+    return owner_sum(contrib, world, n, scale, out_avg, out_sum, nullptr, sumsq_partials, nullptr, stream);
+}
+
+int z1_owner_sum_bf16_waves(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                            float* out_sum, double* waves, int keep_end, void* stream) {
+    if (!waves && n > 0) return Z1_E_NULL;
+    return owner_sum(contrib, world, n, scale, out_avg, out_sum, waves, nullptr, nullptr, stream, keep_end != 0);
+}
+
+int z1_reduce_waves(const double* waves, int64_t m, double* partials, void* stream) {
+    if (!partials || (m > 0 && !waves)) return Z1_E_NULL;
+    if (m < 0) return Z1_E_SIZE;
+    hipLaunchKernelGGL(reduce_partials_kernel, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0,
+                       static_cast<hipStream_t>(stream), waves, m, partials);
+    return launch_status();
 }
 
 int z1_owner_sum_update(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
                         float* out_sum, double* workspace, const z1_update_scalars* u, void* stream) {
     if (!workspace || !u) return Z1_E_NULL;
-    return owner_sum(contrib, world, n, scale, out_avg, out_sum, workspace, u, stream);
+    return owner_sum(contrib, world, n, scale, out_avg, out_sum, nullptr, workspace, u, stream);
 }
 
 int z1_owner_sum_update_noalloc(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
@@ -1337,7 +1409,7 @@ int z1_owner_sum_update_noalloc(const uint16_t* const* contrib, int world, int64
     if (rc) return rc;
     // every scratch slot this call reads is written by it first (the per-wave partials by the owner sum, the
     // Z1_NORM_PARTIALS partials by their reduction), so nothing needs clearing between calls
-    return owner_sum(contrib, world, n, scale, out_avg, out_sum, ws, u, stream);
+    return owner_sum(contrib, world, n, scale, out_avg, out_sum, nullptr, ws, u, stream);
 }
 
 int z1_scale_up(const uint16_t* g16, float* g32, const float* factor, int64_t n, void* stream) {
@@ -1375,6 +1447,7 @@ const char* z1_strerror(int code) {
         case Z1_E_WORKSPACE: return "workspace too small";
         case Z1_E_DEVICE: return "table used on another device than it was created on";
         case Z1_E_NOALLOC_MAX: return "more than Z1_NOALLOC_MAX_N elements for the no-allocation entry point";
+        case Z1_E_STATE: return "a binding launch on this table failed; rebind it before launching over it";
         default: break;
     }
     if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

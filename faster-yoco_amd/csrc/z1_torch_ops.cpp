@@ -23,6 +23,7 @@
 #include <ATen/ops/empty.h>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
 #include <torch/library.h>
 
 #include <dlfcn.h>
@@ -52,6 +53,9 @@ struct Api {
     decltype(&::z1_owner_sum_bf16) owner_sum_bf16;
     decltype(&::z1_owner_sum_workspace) owner_sum_workspace;
     decltype(&::z1_owner_sum_update) owner_sum_update;
+    decltype(&::z1_owner_sum_bf16_waves) owner_sum_bf16_waves;
+    decltype(&::z1_owner_sum_waves) owner_sum_waves;
+    decltype(&::z1_reduce_waves) reduce_waves;
     decltype(&::z1_grad_sumsq) grad_sumsq;
     decltype(&::z1_update_scalars_run) update_scalars_run;
     decltype(&::z1_grad_update_scalars) grad_update_scalars;
@@ -154,6 +158,9 @@ z1_update_scalars scalars(const char* what, int device, const OptTensor& factor,
 }
 
 // ------------------------------------------------------------------------------------------ tables
+using Bound = std::array<uintptr_t, 6>;   // (g, p, m, v, p16, FP32 gradient output) of one row
+constexpr uintptr_t kUnknown = ~static_cast<uintptr_t>(0);   // a binding no call can match: rebind at the next call
+
 struct TableState {
     z1_table* h = nullptr;
     int device = 0;
@@ -163,8 +170,11 @@ struct TableState {
     std::vector<int64_t> sizes;
     std::vector<int64_t> offsets;                    // flat form: element offset of each row in its buffers
     int64_t flat_need = 0;                           // flat form: elements a buffer must hold
-    std::vector<std::array<uintptr_t, 6>> bound;     // (g, p, m, v, p16, FP32 gradient output) per row, as the
-};                                                   // device table holds them
+    std::vector<Bound> bound;                        // per row, what the device table holds once the launches
+                                                     // enqueued so far have run (kUnknown: not known)
+    void* last_stream = nullptr;                     // the stream of the table's last eager launch
+    hipEvent_t handoff = nullptr;                    // orders a call on another stream after that stream's work
+};
 
 std::unordered_map<uintptr_t, TableState> g_tables;
 
@@ -220,66 +230,116 @@ void column(const TableState& t, TensorList lst, int k, const char* what, std::v
     }
 }
 
+bool capturing(void* stream) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    return hipStreamIsCapturing(static_cast<hipStream_t>(stream), &st) == hipSuccess &&
+           st != hipStreamCaptureStatusNone;
+}
+
+void forget_binding(TableState& t) {
+    for (Bound& b : t.bound) b.fill(kUnknown);
+}
+
+// Orders this call after everything already enqueued on the stream the table was last launched on, when that is
+// another stream: the device rows are shared by every launch over the table, and the rebind this call may enqueue
+// must not rewrite them under a launch still running there (an event recorded on that stream now, waited for on
+// this one; no host synchronisation).  The reference has no such shared state: each of its launches carries its own
+// pointers (yoco/tasks/fused_adam_cast.py:68-70).
+void order_after_last_stream(TableState& t, void* stream) {
+    if (t.last_stream == nullptr || t.last_stream == stream) return;
+    hipError_t e = hipSuccess;
+    if (!t.handoff) e = hipEventCreateWithFlags(&t.handoff, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventRecord(t.handoff, static_cast<hipStream_t>(t.last_stream));
+    if (e == hipSuccess) e = hipStreamWaitEvent(static_cast<hipStream_t>(stream), t.handoff, 0);
+    TORCH_CHECK(e == hipSuccess, "yoco_z1: ordering a table's call after its previous stream failed: ",
+                hipGetErrorString(e));
+}
+
 // Points the device table at the call's tensors, enqueuing a rebind on the stream only when an address moved.
 // pmv16: the p, m, v, p16 lists, or nullptr to keep their binding; gout: the FP32 gradient outputs (an empty list:
 // none), or nullptr to keep them (the norm reads no output).
+//
+// Under stream capture the call always enqueues the binding of every column it reads (the gradients for the norm;
+// every column, and the outputs when given, for Adam), so that each replay of the graph points the table at the
+// tensors it was captured with, whatever eager calls did to the table in between; those columns of the recorded
+// binding are then forgotten, so the next eager call rebinds them too.  A failed binding launch forgets the whole
+// binding (the device rows may be half rewritten).
 void bind(TableState& t, TensorList g, const TensorList* pmv16, const TensorList* gout, const char* what,
           void* stream) {
     const size_t nr = t.sizes.size();
     if (nr == 0) return;
+    const bool cap = capturing(stream);
     thread_local std::vector<uintptr_t> cols[6];
     column(t, g, 0, what, cols[0]);
     for (int k = 1; k < 6; ++k) {
         const TensorList* given = k < 5 ? (pmv16 ? &pmv16[k - 1] : nullptr) : gout;
         if (given) {
             column(t, *given, k, what, cols[k]);
-        } else {
+        } else {                                      // a column this call does not read: left as bound
             cols[k].resize(nr);
             for (size_t i = 0; i < nr; ++i) cols[k][i] = t.bound[i][k];
         }
     }
-    if (t.has_pmv) {
+    if (t.has_pmv && pmv16) {
         for (size_t i = 0; i < nr; ++i)
             TORCH_CHECK(t.sizes[i] == 0 || (cols[1][i] && cols[2][i] && cols[3][i]), what,
                         ": the table updates masters and moments; every row needs p, m and v");
     }
-    bool moved = false, others = false, outs = false;
+    if (!cap) order_after_last_stream(t, stream);
+    bool moved = cap, others = cap && pmv16 != nullptr, outs = cap && gout != nullptr;
     for (size_t i = 0; i < nr; ++i) {
         moved |= cols[0][i] != t.bound[i][0];
         for (int k = 1; k < 5; ++k) others |= cols[k][i] != t.bound[i][k];
-        outs |= cols[5][i] != t.bound[i][5];
+        outs |= gout != nullptr && cols[5][i] != t.bound[i][5];
     }
-    if (moved && !others) {
-        thread_local std::vector<const void*> gp;
-        gp.assign(nr, nullptr);
-        for (size_t i = 0; i < nr; ++i) gp[i] = reinterpret_cast<const void*>(cols[0][i]);
-        check_rc(api().table_set_grads(t.h, gp.data(), static_cast<int>(nr), stream), "z1_table_set_grads");
-    } else if (others) {
-        thread_local std::vector<z1_tensor> rows;
-        rows.resize(nr);
-        for (size_t i = 0; i < nr; ++i) {
-            rows[i].g = reinterpret_cast<const void*>(cols[0][i]);
-            rows[i].p = reinterpret_cast<float*>(cols[1][i]);
-            rows[i].m = reinterpret_cast<float*>(cols[2][i]);
-            rows[i].v = reinterpret_cast<float*>(cols[3][i]);
-            rows[i].p16 = reinterpret_cast<uint16_t*>(cols[4][i]);
-            rows[i].n = t.sizes[i];
+    try {
+        if (moved && !others) {
+            thread_local std::vector<const void*> gp;
+            gp.assign(nr, nullptr);
+            for (size_t i = 0; i < nr; ++i) gp[i] = reinterpret_cast<const void*>(cols[0][i]);
+            check_rc(api().table_set_grads(t.h, gp.data(), static_cast<int>(nr), stream), "z1_table_set_grads");
+        } else if (others) {
+            thread_local std::vector<z1_tensor> rows;
+            rows.resize(nr);
+            for (size_t i = 0; i < nr; ++i) {
+                rows[i].g = reinterpret_cast<const void*>(cols[0][i]);
+                rows[i].p = reinterpret_cast<float*>(cols[1][i]);
+                rows[i].m = reinterpret_cast<float*>(cols[2][i]);
+                rows[i].v = reinterpret_cast<float*>(cols[3][i]);
+                rows[i].p16 = reinterpret_cast<uint16_t*>(cols[4][i]);
+                rows[i].n = t.sizes[i];
+            }
+            check_rc(api().table_rebind(t.h, rows.data(), static_cast<int>(nr), stream), "z1_table_rebind");
         }
-        check_rc(api().table_rebind(t.h, rows.data(), static_cast<int>(nr), stream), "z1_table_rebind");
+        if (outs) {
+            bool any = false;
+            thread_local std::vector<float*> op;
+            op.assign(nr, nullptr);
+            for (size_t i = 0; i < nr; ++i) {
+                op[i] = reinterpret_cast<float*>(cols[5][i]);
+                any |= op[i] != nullptr;
+            }
+            check_rc(api().table_set_grad_out(t.h, any ? op.data() : nullptr, static_cast<int>(nr), stream),
+                     "z1_table_set_grad_out");
+        }
+    } catch (...) {
+        forget_binding(t);
+        throw;
     }
-    if (outs) {
-        bool any = false;
-        thread_local std::vector<float*> op;
-        op.assign(nr, nullptr);
+    if (cap) {
         for (size_t i = 0; i < nr; ++i) {
-            op[i] = reinterpret_cast<float*>(cols[5][i]);
-            any |= op[i] != nullptr;
+            t.bound[i][0] = kUnknown;
+            if (pmv16)
+                for (int k = 1; k < 5; ++k) t.bound[i][k] = kUnknown;
+            if (gout) t.bound[i][5] = kUnknown;
         }
-        check_rc(api().table_set_grad_out(t.h, any ? op.data() : nullptr, static_cast<int>(nr), stream),
-                 "z1_table_set_grad_out");
+        return;
     }
     for (size_t i = 0; i < nr; ++i)
-        for (int k = 0; k < 6; ++k) t.bound[i][k] = cols[k][i];
+        for (int k = 0; k < 5; ++k) t.bound[i][k] = cols[k][i];
+    if (gout)
+        for (size_t i = 0; i < nr; ++i) t.bound[i][5] = cols[5][i];
+    t.last_stream = stream;
 }
 
 // A table operator's frame: the registry lock, the table, its device current, torch's current stream there.
@@ -505,9 +565,11 @@ void owner_sum_update_(TensorList contribs, const Tensor& out, const Tensor& wor
 
 // The owner sum in the reference's staging layout (yoco/models/decoder/ce_reduce.py:59-74): the contribution of
 // peer k < rank in slot k of `staging`, of k > rank in slot k - 1, rank's own in `out`, summed in rank order into
-// out[base:end].
+// out[base:end].  With `waves` (at least z1_owner_sum_waves(end - base) float64), the norm of the range's average
+// is left there per chunk (z1_owner_sum_bf16_waves), for reduce_waves_; keep_end as z1_owner_sum_bf16_waves takes it
+// (without waves the range's end is always kept).
 void sum_slots_(const Tensor& staging, const Tensor& out, int64_t G, int64_t base, int64_t end, int64_t rank,
-                double scale, int64_t world) {
+                double scale, int64_t world, const OptTensor& waves, bool keep_end) {
     TORCH_CHECK(staging.defined() && staging.is_cuda() && staging.scalar_type() == at::kBFloat16 &&
                 staging.is_contiguous(), "ce_reduce: staging must be a contiguous bf16 GPU tensor");
     TORCH_CHECK(out.defined() && out.is_cuda() && out.scalar_type() == at::kBFloat16 && out.is_contiguous(),
@@ -518,6 +580,9 @@ void sum_slots_(const Tensor& staging, const Tensor& out, int64_t G, int64_t bas
     TORCH_CHECK(0 <= base && base <= end && end <= G && out.numel() >= G && staging.numel() >= (world - 1) * G,
                 "ce_reduce: range [", base, ", ", end, ") does not fit G=", G, ", out ", out.numel(), ", staging ",
                 staging.numel());
+    double* wp = nullptr;
+    if (waves.has_value() && waves->defined())
+        wp = partials_ptr(*waves, "sum_slots", out.device().index(), api().owner_sum_waves(end - base));
     if (end == base) return;
     const uint16_t* s0 = static_cast<const uint16_t*>(staging.data_ptr());
     uint16_t* o0 = static_cast<uint16_t*>(out.data_ptr());
@@ -525,8 +590,24 @@ void sum_slots_(const Tensor& staging, const Tensor& out, int64_t G, int64_t bas
     for (int64_t k = 0; k < world; ++k)
         ptrs[k] = k < rank ? s0 + k * G + base : (k == rank ? o0 + base : s0 + (k - 1) * G + base);
     OnDevice on(out);
-    check_rc(api().owner_sum_bf16(ptrs, static_cast<int>(world), end - base, static_cast<float>(scale), o0 + base,
-                                  nullptr, nullptr, on.stream), "z1_owner_sum_bf16");
+    if (wp)
+        check_rc(api().owner_sum_bf16_waves(ptrs, static_cast<int>(world), end - base, static_cast<float>(scale),
+                                            o0 + base, nullptr, wp, keep_end ? 1 : 0, on.stream),
+                 "z1_owner_sum_bf16_waves");
+    else
+        check_rc(api().owner_sum_bf16(ptrs, static_cast<int>(world), end - base, static_cast<float>(scale),
+                                      o0 + base, nullptr, nullptr, on.stream), "z1_owner_sum_bf16");
+}
+
+// The fixed-order reduction of per-chunk norm partials (the first m of `waves`) into the norm's partials.
+void reduce_waves_(const Tensor& waves, int64_t m, const Tensor& partials) {
+    require_gpu(partials, "reduce_waves");
+    const int dev = partials.device().index();
+    TORCH_CHECK(m >= 0, "yoco_z1: reduce_waves: negative count");
+    double* wp = partials_ptr(waves, "reduce_waves", dev, m);
+    double* part = partials_ptr(partials, "reduce_waves", dev);
+    OnDevice on(partials);
+    check_rc(api().reduce_waves(wp, m, part, on.stream), "z1_reduce_waves");
 }
 
 // ------------------------------------------------------------------------------------------ scale / cast
@@ -609,7 +690,8 @@ void refuse_cpu(const c10::OperatorHandle& op, torch::jit::Stack*) {
 const char* const kOps[] = {
     "grad_sumsq_", "norm_clip_", "grad_norm_clip_", "update_scalars_", "grad_update_scalars_", "clip_factor_",
     "adam_cast_", "adam_cast_gout_", "adam_cast_dev_", "bias_corrections_step_", "owner_sum_", "owner_sum_update_",
-    "sum_slots_", "scale_up_", "cast_bf16_", "embedding_dense_backward_out_", "embedding_dense_backward",
+    "sum_slots_", "reduce_waves_", "scale_up_", "cast_bf16_", "embedding_dense_backward_out_",
+    "embedding_dense_backward",
 };
 
 }  // namespace
@@ -646,7 +728,8 @@ TORCH_LIBRARY(yoco_z1, m) {
           "Tensor(a8!)? flags, Tensor(a9!)? clip_log, Tensor? sample_size, float numer, float max_norm, "
           "float? factor_value) -> ()");
     m.def("sum_slots_(Tensor staging, Tensor(a1!) out, int G, int base, int end, int rank, float scale, "
-          "int world) -> ()");
+          "int world, Tensor(a8!)? waves=None, bool keep_end=True) -> ()");
+    m.def("reduce_waves_(Tensor waves, int m, Tensor(a2!) partials) -> ()");
     m.def("scale_up_(Tensor g16, Tensor(a1!) g32, Tensor factor) -> ()");
     m.def("cast_bf16_(Tensor p32, Tensor(a1!) p16) -> ()");
     m.def("embedding_dense_backward_out_(Tensor grad, Tensor indices, int num_weights, int padding_idx, "
@@ -669,6 +752,7 @@ TORCH_LIBRARY_IMPL(yoco_z1, CUDA, m) {
     m.impl("owner_sum_", &owner_sum_);
     m.impl("owner_sum_update_", &owner_sum_update_);
     m.impl("sum_slots_", &sum_slots_);
+    m.impl("reduce_waves_", &reduce_waves_);
     m.impl("scale_up_", &scale_up_);
     m.impl("cast_bf16_", &cast_bf16_);
     m.impl("embedding_dense_backward_out_", &embedding_dense_backward_out_);
@@ -698,6 +782,9 @@ int z1t_init(const char* path) {
     Z1T_RESOLVE(owner_sum_bf16, z1_owner_sum_bf16)
     Z1T_RESOLVE(owner_sum_workspace, z1_owner_sum_workspace)
     Z1T_RESOLVE(owner_sum_update, z1_owner_sum_update)
+    Z1T_RESOLVE(owner_sum_bf16_waves, z1_owner_sum_bf16_waves)
+    Z1T_RESOLVE(owner_sum_waves, z1_owner_sum_waves)
+    Z1T_RESOLVE(reduce_waves, z1_reduce_waves)
     Z1T_RESOLVE(grad_sumsq, z1_grad_sumsq)
     Z1T_RESOLVE(update_scalars_run, z1_update_scalars_run)
     Z1T_RESOLVE(grad_update_scalars, z1_grad_update_scalars)
@@ -734,9 +821,9 @@ int z1t_table_register(z1_table* table, int device, int g_dtype, int has_pmv, in
     for (int i = 0; i < nrows; ++i) {
         if (rows[i].n < 0) return -1;
         t.sizes[i] = rows[i].n;
-        t.bound[i] = {reinterpret_cast<uintptr_t>(rows[i].g), reinterpret_cast<uintptr_t>(rows[i].p),
-                      reinterpret_cast<uintptr_t>(rows[i].m), reinterpret_cast<uintptr_t>(rows[i].v),
-                      reinterpret_cast<uintptr_t>(rows[i].p16), 0};          // no gradient outputs yet
+        t.bound[i] = Bound{reinterpret_cast<uintptr_t>(rows[i].g), reinterpret_cast<uintptr_t>(rows[i].p),
+                           reinterpret_cast<uintptr_t>(rows[i].m), reinterpret_cast<uintptr_t>(rows[i].v),
+                           reinterpret_cast<uintptr_t>(rows[i].p16), 0};     // no gradient outputs yet
     }
     if (t.flat) {
         t.offsets.assign(offsets, offsets + nrows);
@@ -753,7 +840,10 @@ int z1t_table_register(z1_table* table, int device, int g_dtype, int has_pmv, in
 /* Forgets a table (before z1_table_destroy). */
 void z1t_table_forget(z1_table* table) {
     std::lock_guard<std::mutex> lock(g_mu);
-    g_tables.erase(reinterpret_cast<uintptr_t>(table));
+    auto it = g_tables.find(reinterpret_cast<uintptr_t>(table));
+    if (it == g_tables.end()) return;
+    if (it->second.handoff) (void)hipEventDestroy(it->second.handoff);
+    g_tables.erase(it);
 }
 
 }  // extern "C"

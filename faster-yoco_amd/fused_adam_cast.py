@@ -9,7 +9,8 @@ arguments, and collects in ``.cast`` the addresses of the masters whose BF16 cop
   * what a parameter list needs -- its tables, the BF16 destinations found in ``dest``, the masters they belong to
     -- is worked out once per list of masters and set of folded rows (keyed by the masters' addresses and sizes,
     as ``dest`` is keyed by address) and reused while they recur; each call's tensors are still checked, by the
-    operator;
+    operator; a table's rows are ordered by their gradients' addresses (the launch starts at the highest, which is
+    what the pass before it wrote last);
   * ``fold`` / ``fold_factor`` (set by zero1_fast.step with the fused Adam) name masters whose BF16 gradient the
     kernel reads times the factor, in place of the FP32 gradient a scale pass would have written first: the same
     products g' = fp32(float(g16) * factor).  With ``fold_writes`` (zero1_fast's default) the kernel also stores
@@ -99,9 +100,16 @@ class FusedAdamCast:
         groups = []
         for f in (False, True):
             if rows[f]:
-                table = self._tables.get(rows[f], rows[f][0][1].device)
-                whole = len(idx[f]) == len(key)
-                groups.append((f, None if whole else tuple(idx[f]), table, ops.rows_lists(rows[f])[4]))
+                # rows in the order of their gradients' addresses: the launch walks from the last row down, so it
+                # starts at the highest gradient address -- the end of a flat gradient buffer, which the owner sum
+                # that wrote it last left in the MALL (CEReduce's last phase, ce_reduce.py:227) -- whatever order
+                # the parameters come in (CEReduce lays them out by backward phase, :122-140)
+                order = sorted(range(len(rows[f])), key=lambda j: rows[f][j][0].data_ptr())
+                srows = [rows[f][j] for j in order]
+                sidx = [idx[f][j] for j in order]
+                table = self._tables.get(srows, srows[0][1].device)
+                whole = sidx == list(range(len(key)))
+                groups.append((f, None if whole else tuple(sidx), table, ops.rows_lists(srows)[4]))
         plan = (tuple(groups), tuple(written))
         self._plans[(key, folded)] = plan
         while len(self._plans) > 8:

@@ -154,7 +154,9 @@ class TableCache:
     bind a table to each call's tensors (a rebind launch only when addresses moved), so steps whose
     gradients autograd reallocates neither allocate nor synchronise; the cache's tables keep no default tensors,
     so callers pass them (``ops.adam_cast(..., tensors=ops.rows_lists(rows))``, ``ops.grad_sumsq(..., g=grads)``).
-    ``builds`` counts the tables made."""
+    An evicted table is only dropped from the cache: a caller that still holds it (``FusedAdamCast``'s plans do)
+    keeps using it, and it is freed with its last reference (``Table.__del__``).  ``builds`` counts the tables
+    made."""
 
     def __init__(self, capacity=8):
         self.capacity = capacity
@@ -171,14 +173,12 @@ class TableCache:
             self.builds += 1            # to a step's gradients, so their memory is free for the next step's)
             self._d[key] = t
             while len(self._d) > self.capacity:
-                self._d.popitem(last=False)[1].close()
+                self._d.popitem(last=False)
         else:
             self._d.move_to_end(key)
         return t
 
     def clear(self):
-        for t in self._d.values():
-            t.close()
         self._d.clear()
 
 

@@ -67,8 +67,9 @@ def _embedding_fake(grad, indices, num_weights, padding_idx, scale, scale_mode, 
 
 
 OPS = ('grad_sumsq_', 'norm_clip_', 'grad_norm_clip_', 'update_scalars_', 'grad_update_scalars_', 'clip_factor_',
-       'adam_cast_', 'adam_cast_gout_', 'adam_cast_dev_', 'bias_corrections_step_', 'owner_sum_', 'owner_sum_update_', 'sum_slots_',
-       'scale_up_', 'cast_bf16_', 'embedding_dense_backward_out_', 'embedding_dense_backward')
+       'adam_cast_', 'adam_cast_gout_', 'adam_cast_dev_', 'bias_corrections_step_', 'owner_sum_', 'owner_sum_update_',
+       'sum_slots_', 'reduce_waves_', 'scale_up_', 'cast_bf16_', 'embedding_dense_backward_out_',
+       'embedding_dense_backward')
 
 for _name in OPS:
     torch.library.register_fake(f'{NS}::{_name}',

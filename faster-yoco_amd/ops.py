@@ -144,9 +144,22 @@ def owner_sum_update(contribs, out, scale, workspace, out_sum=None, sample_size=
                            flags_out, clip_log_out, sample_size, f32(numer), f32(max_norm), fv)
 
 
-def sum_slots(S, OUT, G, BASE, END, R, scale, WORLD):
-    """The owner sum in the reference's staging layout, in place (yoco/models/decoder/ce_reduce.py:59-74)."""
-    _OPS.sum_slots_(S, OUT, int(G), int(BASE), int(END), int(R), f32(scale), int(WORLD))
+def sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=None, keep_end=True):
+    """The owner sum in the reference's staging layout, in place (yoco/models/decoder/ce_reduce.py:59-74).  waves
+    (float64, at least owner_sum_waves(END - BASE)): the range's norm partials per chunk, for reduce_waves.
+    keep_end (with waves): leave the range's last 224 MB in the MALL for the pass that reads them next."""
+    _OPS.sum_slots_(S, OUT, int(G), int(BASE), int(END), int(R), f32(scale), int(WORLD), waves, bool(keep_end))
+
+
+def owner_sum_waves(n):
+    """Per-chunk norm partials an owner sum over n elements leaves (sum_slots' waves)."""
+    return int(lib().z1_owner_sum_waves(int(n)))
+
+
+def reduce_waves(waves, m, partials):
+    """The first m per-chunk partials of waves, reduced in a fixed order into the norm partials (norm_workspace)
+    that norm_clip / update_scalars read."""
+    _OPS.reduce_waves_(waves, int(m), partials)
 
 
 # ------------------------------------------------------------------------------------------------ scale / cast

@@ -174,14 +174,27 @@ def clip_grad_norm(self, max_norm, aggregate_norm_fn=None):
     out = factor if torch.is_tensor(factor) else torch.empty(1, dtype=torch.float32, device=dev)
     grad_norm = torch.empty(1, dtype=torch.float32, device=dev)
     clip = float(max_norm) if max_norm > 0.0 else 0.0
-    table = plan.norm_tables.get([(g, None, None, None, None, g.numel()) for g in grads], dev) if grads else None
-    if REDUCE_OWNER and plan.world == 1 and aggregate_norm_fn is None and table is not None:
+    # the owned gradients are the average CEReduce's phase sums wrote: their norm partials are already there
+    fused = ce_reduce.take_norm_partials(grads) if REDUCE_OWNER else None
+    table = None
+    if fused is None and grads:
+        # rows in the order of the gradients' addresses: the pass reads the last 256 MB of its table with
+        # allocating loads, which should be what the fused Adam reads first (it starts at the highest address)
+        grads = sorted(grads, key=lambda g: g.data_ptr())
+        table = plan.norm_tables.get([(g, None, None, None, None, g.numel()) for g in grads], dev)
+    one_owner = REDUCE_OWNER and plan.world == 1 and aggregate_norm_fn is None and (grads or fused)
+    if one_owner and fused is not None:
         # one owner: the all-reduce of n_r^2 is the identity, and the kernel's chain is the reference's
-        # (sq = n_r^2, norm = sqrt(sq), grad_norm, clip), so norm and clip are one call
+        # (sq = n_r^2, norm = sqrt(sq), grad_norm, clip)
+        ops.reduce_waves(fused[0], fused[1], plan.partials)
+        ops.norm_clip(plan.partials, factor=factor, grad_norm_out=grad_norm, factor_out=out, max_norm=clip)
+    elif one_owner:
         ops.grad_norm_clip(table, plan.partials, factor=factor, grad_norm_out=grad_norm, factor_out=out,
-                           max_norm=clip, g=grads)
+                           max_norm=clip, g=grads)                  # norm and clip in one call
     else:
-        if table is not None:
+        if fused is not None:
+            ops.reduce_waves(fused[0], fused[1], plan.partials)
+        elif table is not None:
             ops.grad_sumsq(table, plan.partials, g=grads)
         else:
             plan.partials.zero_()

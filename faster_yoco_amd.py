@@ -1,6 +1,7 @@
 """Import name of the package in faster-yoco_amd/, whose directory name is not a Python identifier: with the
 repository root on sys.path, ``import faster_yoco_amd`` (or ``from faster_yoco_amd import zero1_fast``) loads that
-package under this name.  Importing it does not load the native library; the operations do, on first use."""
+package under this name.  Importing it loads the native libraries (built in-tree by __graft_entry__.build()) and
+registers the PyTorch operators; a missing library raises RuntimeError."""
 import importlib.util
 import os
 import sys

@@ -36,6 +36,9 @@ enum {
     Z1_E_WORKSPACE = -6,   /* workspace too small */
     Z1_E_DEVICE = -7,      /* table used on a device other than the one it was created on */
     Z1_E_NOALLOC_MAX = -8, /* input larger than the no-allocation entry point's fixed scratch */
+    Z1_E_STATE = -9,       /* a binding launch on the table failed (its device rows may be half rewritten): launches
+                              over it are refused until z1_table_rebind (rows) / z1_table_set_grad_out (outputs)
+                              succeeds */
 };
 
 enum { Z1_F32 = 0, Z1_BF16 = 1 };           /* gradient dtype codes */
@@ -110,8 +113,28 @@ int z1_table_rebind(z1_table* table, const z1_tensor* rows, int nrows, void* str
 int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
                       float* out_sum, double* sumsq_partials, void* stream);
 /* Doubles the fused-norm workspace of z1_owner_sum_bf16 / z1_owner_sum_update must hold for n elements
- * (negative: error code). */
+ * (negative: error code): Z1_NORM_PARTIALS + z1_owner_sum_waves(n). */
 int64_t z1_owner_sum_workspace(int64_t n);
+/* Per-chunk norm partials an owner sum over n elements writes (negative: error code).  The chunk grid follows the
+ * streams' addresses (boundaries on shared 128-byte lines, else on 8-byte words, so that a range starting anywhere
+ * keeps the vector path); this count covers every grid. */
+int64_t z1_owner_sum_waves(int64_t n);
+
+/* z1_owner_sum_bf16 with the fused norm left per chunk: waves (z1_owner_sum_waves(n) doubles) receives each chunk's
+ * FP64 sum of squares of the BF16 average (a fixed decomposition; nothing is reduced).  For a caller that sums a
+ * gradient buffer one range at a time -- CEReduce._sum, once per backward phase
+ * (yoco/models/decoder/ce_reduce.py:178-183,205-209,227) -- and wants the norm of the whole buffer without reading
+ * it again, as yoco/tasks/zero1_fast.py:150 does: the ranges' partials, side by side in one array, go to
+ * z1_reduce_waves once.  keep_end: the range's end is what the next pass reads first (the Adam launches walk their
+ * gradients from the highest address down), so its last 224 MB are stored with allocating stores and stay in the
+ * 256 MB MALL (z1_owner_sum_bf16 always does this); 0 for a range summed long before the update, all stores
+ * streaming.  No counterpart in the reference, whose screen of a norm fused into the sum was not adopted
+ * (docs/training.md:335); the values are the same. */
+int z1_owner_sum_bf16_waves(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
+                            float* out_sum, double* waves, int keep_end, void* stream);
+/* Fixed-order reduction of m per-chunk partials (z1_owner_sum_bf16_waves) into the Z1_NORM_PARTIALS partials that
+ * z1_norm_clip and z1_update_scalars_run read. */
+int z1_reduce_waves(const double* waves, int64_t m, double* partials, void* stream);
 
 /* Multi-tensor sum of squares of the table's gradients (the norm of fairseq utils.clip_grad_norm_ ->
  * apex multi_tensor_l2norm, called at yoco/tasks/zero1_fast.py:150,157): per-workgroup FP64 partials over a fixed

@@ -67,7 +67,18 @@ def test_argument_errors_without_device_work(pkg):
     assert L.z1_cast_bf16(None, None, 4, None) == -1
     assert L.z1_table_destroy(None) == 0
     assert L.z1_owner_sum_workspace(-1) == -2
-    assert [L.z1_owner_sum_workspace(n) for n in (0, 1, 256, 257, 513)] == [2048, 2049, 2049, 2050, 2051]
+    # one partial per 256-element chunk of a grid that may be shifted by up to 63 elements (to the streams' lines)
+    sizes = (0, 1, 193, 194, 256, 257, 449, 450, 513)
+    assert [L.z1_owner_sum_waves(n) for n in sizes] == [0, 1, 1, 2, 2, 2, 2, 3, 3]
+    assert [L.z1_owner_sum_workspace(n) - 2048 for n in sizes] == [L.z1_owner_sum_waves(n) for n in sizes]
+    assert L.z1_owner_sum_waves(-1) == -2
+    assert L.z1_owner_sum_bf16_waves(ctypes.cast(arr, ctypes.c_void_p), 1, 10, 1.0, ctypes.c_void_p(32), None, None,
+                                     1, None) == -1                                # no partials array
+    assert L.z1_owner_sum_bf16_waves(ctypes.cast(arr, ctypes.c_void_p), 0, 10, 1.0, ctypes.c_void_p(32), None,
+                                     ctypes.c_void_p(64), 1, None) == -4
+    assert L.z1_reduce_waves(None, 4, ctypes.c_void_p(64), None) == -1
+    assert L.z1_reduce_waves(ctypes.c_void_p(32), 4, None, None) == -1
+    assert L.z1_reduce_waves(ctypes.c_void_p(32), -1, ctypes.c_void_p(64), None) == -2
     assert L.z1_grad_norm_clip(None, None, None, 1.0, None, None, None, 1.0, None) == -1
     assert L.z1_grad_update_scalars(None, None, None, None) == -1
     assert L.z1_table_set_grads(None, None, 0, None) == -1

@@ -94,6 +94,45 @@ def test_fused_adam_cast_errors(pkg, dev):
     fa(0, None, [[], [], [], []], 1e-3, 0.9, 0.95, 1e-8, 2, 1, 1, 0.0)          # empty lists: nothing to do
 
 
+def test_fused_adam_cast_plans_outlive_the_table_cache(pkg, dev):
+    """More table signatures than the table cache holds (5 parameter lists, each with folded and unfolded rows: 10
+    tables, the cache keeps 8), cycled twice through FusedAdamCast's plan cache: a plan keeps its tables alive after
+    the cache evicted them, and every call matches the oracle bit for bit."""
+    from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+    fa = FusedAdamCast({})
+    factor = torch.full((1,), 0.5, dtype=torch.float32, device=dev)
+    rng = np.random.default_rng(17)
+    lists = []
+    for k in range(5):
+        rows = []
+        for n in (64 * (k + 1) + 3, 40 + 7 * k):
+            g16 = oracle.bf16_rne((rng.standard_normal(n) * 1e-3).astype(np.float32))
+            g32 = (rng.standard_normal(n) * 1e-3).astype(np.float32)
+            p = (rng.standard_normal(n) * 0.02).astype(np.float32)
+            rows.append({'g16': g16, 'g32': g32, 'p': p, 'm': np.zeros(n, np.float32), 'v': np.zeros(n, np.float32),
+                         't': [torch.from_numpy(x).to(dev) for x in (g32, p, np.zeros(n, np.float32),
+                                                                      np.zeros(n, np.float32))],
+                         'g16t': torch.from_numpy(g16.view(np.int16)).to(dev).view(torch.bfloat16)})
+        lists.append(rows)
+    for rnd in range(2):
+        for rows in lists:
+            step = rnd + 1
+            fa.fold = {rows[0]['t'][1].data_ptr(): rows[0]['g16t']}
+            fa.fold_factor, fa.fold_writes = factor, False
+            fa(0, None, [[r['t'][k] for r in rows] for k in range(4)], HP['lr'], HP['beta1'], HP['beta2'],
+               HP['eps'], step, 1, 1, HP['weight_decay'])
+            torch.cuda.synchronize()
+            for i, r in enumerate(rows):
+                g, f = (r['g16'], 0.5) if i == 0 else (r['g32'], None)
+                po, mo, vo, _ = oracle.adam_cast(g, r['p'], r['m'], r['v'], step=step, factor=f, **HP)
+                assert np.array_equal(bits(r['t'][1]), po.view(np.uint32)), (rnd, i)
+                assert np.array_equal(bits(r['t'][2]), mo.view(np.uint32)), (rnd, i)
+                assert np.array_equal(bits(r['t'][3]), vo.view(np.uint32)), (rnd, i)
+                r['p'], r['m'], r['v'] = po, mo, vo
+    assert fa._tables.builds == 10
+    fa.fold, fa.fold_factor = {}, None
+
+
 # ---------------------------------------------------------------------------------------------- zero1_fast
 def expected_update(params, grads16, state, step, factor0, max_norm, reduce_owner):
     """Oracle: norm over all bf16 grads and the clip chain of zero1_fast.py:150-160 (REDUCE_OWNER: via sq and
@@ -309,3 +348,99 @@ def test_zero1_fast_measured_switch_set_with_placed_params(pkg, dev):
         zero1_fast.configure(ENABLED=False, ALLGATHER=False, PARAM_VIEWS=False, REDUCE_OWNER=False)
         zero1_fast._PLACED.clear()
         dist.destroy_process_group()
+
+
+def test_ce_reduce_phase_norm_feeds_clip_grad_norm(pkg, dev, monkeypatch):
+    """The reference's measured switch set with YOCO_CE_REDUCE: CEReduce._sum per phase (two on a side stream, the
+    last on the current one, yoco/models/decoder/ce_reduce.py:205-209,227-228), the owned gradients made views of
+    CEReduce.out (:232-237), then zero1_fast.clip_grad_norm and step.  The norm comes from the partials the phase
+    sums left -- no norm pass over the gradients runs -- and is within one fp32 ulp of the norm pass over the same
+    gradients (and 1e-6 of the exact norm); the clip chain, the written FP32 gradients, masters, moments and BF16
+    copies match the oracle bit for bit.  Gradients that are not those views (a zero-filled one, or a phase that was
+    not summed this update) take the norm pass instead."""
+    from faster_yoco_amd import ce_reduce, layout, ops, zero1_fast
+    zero1_fast.configure(ENABLED=True, ALLGATHER=True, PARAM_VIEWS=True, REDUCE_OWNER=True, ONE_PASS=True,
+                         SCALE_KERNEL=True, FUSED_ADAM=True, FOLD_SCALE=False)
+    zero1_fast._PLACED.clear()
+    try:
+        params = bf16_params(dev, 11)
+        zero1_fast._PLACED.update(layout.place_params(params, 1))
+
+        class Mixin(fakes.FakeMixin):
+            pass
+
+        zero1_fast._ORIG.clear()
+        zero1_fast.install(Mixin)
+
+        class Opt(Mixin, fakes.FakeFP16Optimizer):
+            pass
+
+        opt = Opt(params, lr=HP['lr'], betas=(HP['beta1'], HP['beta2']), eps=HP['eps'],
+                  weight_decay=HP['weight_decay'])
+        numels = [p.numel() for p in params]
+        G, W, R = sum(numels), 8, 2
+        ends = np.cumsum(numels).tolist()
+        bounds = [[0, ends[1]], [ends[1], ends[1]], [ends[1], ends[3]], [ends[3], G]]   # an empty phase too
+        cls = ce_reduce.install(type('CEReduce', (fakes.FakeCEReduce,), {}))
+        rng = np.random.default_rng(4)
+        state = [(p.detach().float().cpu().numpy().ravel().copy(), np.zeros(p.numel(), np.float32),
+                  np.zeros(p.numel(), np.float32)) for p in params]
+        side = torch.cuda.Stream(device=dev)
+        used = {'pass': 0}
+        for name in ('grad_sumsq', 'grad_norm_clip'):
+            real = getattr(ops, name)
+
+            def counted(*a, _real=real, **k):
+                used['pass'] += 1
+                return _real(*a, **k)
+            monkeypatch.setattr(ops, name, counted)
+        for step, (max_norm, fused) in enumerate(((1.0, True), (0.01, True), (1.0, False), (1.0, 'stale')), 1):
+            S = oracle.bf16_rne((rng.standard_normal((W - 1) * G) * 1e-2).astype(np.float32))
+            OUT = oracle.bf16_rne((rng.standard_normal(G) * 1e-2).astype(np.float32))
+            ce = cls(torch.from_numpy(S.view(np.int16)).to(dev).view(torch.bfloat16),
+                     torch.from_numpy(OUT.view(np.int16)).to(dev).view(torch.bfloat16), G, bounds, R, W)
+            avg = OUT.copy()
+            for a, b in bounds:
+                oracle.sum_slots(S, avg, G, a, b, R, 1.0 / W, W)
+            cur = torch.cuda.current_stream(dev)
+            side.wait_stream(cur)
+            with torch.cuda.stream(side):
+                for ph in range(len(bounds) - 1):
+                    ce._sum(ph)
+            if fused != 'stale':
+                ce._sum(len(bounds) - 1)
+            else:                                  # the last phase summed without its partials: no fused norm
+                ce_reduce.sum_slots(ce.staging, ce.out, G, *bounds[-1], R, 1.0 / W, W)
+            cur.wait_stream(side)
+            off = 0
+            for p, n in zip(params, numels):
+                p.grad = ce.out[off:off + n].view_as(p)
+                off += n
+            if fused is False:
+                params[1].grad = params[1].grad.clone()          # no longer a view of out
+            grads16 = [avg[o - n:o] for o, n in zip(ends, numels)]
+            before = used['pass']
+            gn = opt.clip_grad_norm(max_norm)
+            assert (used['pass'] == before) == (fused is True), step
+            fac = float(opt._multiply_factor.item())
+            _, exp_gn, exp_fac = oracle.norm_clip(sum(oracle.sumsq(g) for g in grads16), 1.0, max_norm)
+            got = np.float32(gn.item())
+            assert abs(int(got.view(np.int32)) - int(exp_gn.view(np.int32))) <= 1, (step, got, exp_gn)
+            if got == exp_gn:                              # same norm bits -> the chain is bit-exact
+                assert np.float32(fac) == exp_fac, step
+            opt.step()
+            torch.cuda.synchronize()
+            for i, p in enumerate(params):
+                po, mo, vo, p16 = oracle.adam_cast(grads16[i], *state[i], step=step, factor=fac, **HP)
+                st = opt.fp32_optimizer.optimizer.optim.state[opt.fp32_params[i]]
+                assert np.array_equal(bits(opt.fp32_params[i].grad).ravel(),
+                                      oracle.scale_up(grads16[i], fac).view(np.uint32)), (step, i)
+                assert np.array_equal(bits(opt.fp32_params[i]).ravel(), po.view(np.uint32)), (step, i)
+                assert np.array_equal(bits(st['exp_avg']).ravel(), mo.view(np.uint32)), (step, i)
+                assert np.array_equal(bits(st['exp_avg_sq']).ravel(), vo.view(np.uint32)), (step, i)
+                assert np.array_equal(bits(p).ravel(), p16), (step, i)
+                state[i] = (po, mo, vo)
+            opt.zero_grad()
+    finally:
+        zero1_fast.configure(ENABLED=False, ALLGATHER=False, PARAM_VIEWS=False, REDUCE_OWNER=False)
+        zero1_fast._PLACED.clear()

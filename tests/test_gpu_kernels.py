@@ -422,6 +422,91 @@ def test_owner_sum_in_place_reference_slot_layout(pkg, dev):
         assert np.array_equal(host_bf16(St), S)
 
 
+# element offsets (average, contributions, fp32 sum) of the streams inside 512-byte-aligned allocations
+MISALIGNED = {
+    'lines_shared_2B': (1, (1, 1, 1, 1), 1),          # every stream 2 bytes into a line: the grid moves by 1
+    'lines_shared_134B': (67, (67, 67, 67, 67), 67),  # 6 bytes into the second line of each
+    'lines_apart_by_128B': (5, (69, 5, 133, 5), None),
+    'words_shared': (1, (5, 1, 9, 13), None),          # same offset within 8-byte words only
+    'no_common_word': (1, (2, 1, 1, 1), None),         # element-wise path
+    'fp32_sum_off_grid': (1, (1, 1, 1, 1), 0),         # the fp32 sum not 16-byte aligned on the grid: element path
+}
+
+
+@pytest.mark.parametrize('case', sorted(MISALIGNED))
+def test_owner_sum_misaligned_ranges(pkg, dev, case):
+    """Streams that start off the 16-byte boundaries -- a CEReduce phase starts at any parameter boundary of the
+    owner's gradient: the chunk grid follows the offset the streams share (a 128-byte line offset, else an 8-byte
+    word offset, else the element-wise path); the average and the fp32 sum stay bit-exact, the fused norm within
+    1e-6 of the exact one."""
+    from faster_yoco_amd import ops
+    oo, co, so = MISALIGNED[case]
+    rng = np.random.default_rng(len(case))
+    n = 3 * 4096 + 45
+    cs = [oracle.bf16_rne((rng.standard_normal(n) * 1e-3).astype(np.float32)) for _ in co]
+    avg, s = oracle.owner_sum(cs, want_sum=True)
+    ts = []
+    for c, off in zip(cs, co):
+        buf = torch.zeros(n + 256, dtype=torch.bfloat16, device=dev)
+        buf[off:off + n].copy_(dev_bf16(c, dev))
+        ts.append(buf[off:off + n])
+    out = torch.zeros(n + 256, dtype=torch.bfloat16, device=dev)[oo:oo + n]
+    osum = None if so is None else torch.zeros(n + 256, dtype=torch.float32, device=dev)[so:so + n]
+    part = ops.norm_workspace(dev, n)
+    ops.owner_sum(ts, out, 1.0 / len(cs), out_sum=osum, partials=part)
+    nr = torch.zeros(1, device=dev)
+    ops.norm_clip(part, norm_out=nr)
+    torch.cuda.synchronize()
+    assert same_bf16(host_bf16(out), avg)
+    if osum is not None:
+        assert same_f32(host_f32(osum), s)
+    ex = float(np.sqrt(oracle.sumsq(avg)))
+    assert abs(float(nr.item()) - ex) <= 1e-6 * ex
+
+
+def test_sum_slots_phase_partials_give_the_norm_of_the_whole_average(pkg, dev):
+    """CEReduce's phases at odd bounds, each summed in place with its norm partials left in its own slice of one
+    array (sum_slots' waves), then one fixed-order reduction: the average bit-exact against the oracle, the norm
+    within one fp32 ulp of the norm pass over the same BF16 average (and within 1e-6 of the exact norm), and the
+    same bits when the phases run again."""
+    from faster_yoco_amd import ce_reduce, ops
+    rng = np.random.default_rng(21)
+    W, R, G = 8, 5, 5 * 4096 + 321
+    bounds = [(0, 4099), (4099, 4099), (4099, 12001), (12001, G)]
+    S = oracle.bf16_rne((rng.standard_normal((W - 1) * G) * 1e-3).astype(np.float32))
+    OUT = oracle.bf16_rne((rng.standard_normal(G) * 1e-3).astype(np.float32))
+    exp = OUT.copy()
+    counts = [ops.owner_sum_waves(b - a) for a, b in bounds]
+    waves = torch.full((sum(counts),), np.nan, dtype=torch.float64, device=dev)
+    norms = []
+    for rep in range(2):
+        St, Ot = dev_bf16(S, dev), dev_bf16(OUT, dev)
+        off = 0
+        for (a, b), c in zip(bounds, counts):
+            ce_reduce.sum_slots(St, Ot, G, a, b, R, 1.0 / W, W, waves=waves[off:off + c])
+            if rep == 0:
+                oracle.sum_slots(S, exp, G, a, b, R, 1.0 / W, W)
+            off += c
+        part = ops.norm_workspace(dev)
+        ops.reduce_waves(waves, off, part)
+        nr = torch.zeros(1, device=dev)
+        ops.norm_clip(part, norm_out=nr)
+        torch.cuda.synchronize()
+        assert np.array_equal(host_bf16(Ot), exp)
+        norms.append(np.float32(nr.item()))
+    assert norms[0].view(np.uint32) == norms[1].view(np.uint32)
+    ex = float(np.sqrt(oracle.sumsq(exp)))
+    assert abs(float(norms[0]) - ex) <= 1e-6 * ex
+    table = ops.Table([(Ot, None, None, None, None, G)], dev)
+    ref = torch.zeros(1, device=dev)
+    part = ops.norm_workspace(dev)
+    ops.grad_sumsq(table, part)
+    ops.norm_clip(part, norm_out=ref)
+    torch.cuda.synchronize()
+    d = abs(int(np.float32(ref.item()).view(np.int32)) - int(norms[0].view(np.int32)))
+    assert d <= 1, (float(ref.item()), float(norms[0]))
+
+
 # ---------------------------------------------------------------------------------------------- scale / cast
 def test_scale_up_and_cast_bit_exact(pkg, dev):
     from faster_yoco_amd import fused_adam_cast, ops

@@ -25,7 +25,7 @@ MUTATES = {
     'adam_cast_dev_': {'p', 'm', 'v', 'p16'}, 'bias_corrections_step_': {'step', 'bc'},
     'owner_sum_': {'out', 'out_sum', 'partials'},
     'owner_sum_update_': {'out', 'workspace', 'out_sum', 'factor', 'norm', 'grad_norm', 'flags', 'clip_log'},
-    'sum_slots_': {'out'}, 'scale_up_': {'g32'}, 'cast_bf16_': {'p16'},
+    'sum_slots_': {'out', 'waves'}, 'reduce_waves_': {'partials'}, 'scale_up_': {'g32'}, 'cast_bf16_': {'p16'},
     'embedding_dense_backward_out_': {'out', 'workspace'}, 'embedding_dense_backward': {'workspace'},
 }
 

@@ -2,12 +2,20 @@
 scratch) against z1_owner_sum_update with a caller workspace, through the C ABI: two calls in a row, the second on a
 smaller input, every output bit-identical (the BF16 average, the FP32 sum, norm, grad_norm, factor, the two flags
 and the clip metric); the same at Z1_NOALLOC_MAX_N elements, where the whole scratch is in use.  Sizes beyond
-Z1_NOALLOC_MAX_N are refused before any device work."""
+Z1_NOALLOC_MAX_N are refused before any device work.  In a fresh process whose first call of the entry point is made
+under HIP graph capture (where the scratch's address is looked up), the replays match the workspace form, and an
+eager call changes neither torch's allocation counters nor the device's free memory."""
 import ctypes
+import os
+import subprocess
+import sys
+import textwrap
 
 import numpy as np
 import pytest
 import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 pytestmark = pytest.mark.gpu
 
@@ -82,3 +90,69 @@ def test_noalloc_refuses_sizes_beyond_its_scratch(pkg, dev):
     rc = L.z1_owner_sum_update_noalloc(ctypes.cast(one, ctypes.c_void_p), 1, _lib.Z1_NOALLOC_MAX_N + 1, 1.0,
                                        ctypes.c_void_p(32), None, ctypes.byref(u), None)
     assert rc == -8 and b'no-allocation' in L.z1_strerror(rc)
+
+
+_CAPTURE_FIRST = textwrap.dedent("""
+    import ctypes, sys
+    import numpy as np
+    import torch
+    sys.path.insert(0, {root!r})
+    sys.path.insert(0, {tests!r})
+    import __graft_entry__
+    __graft_entry__.package()
+    import test_zz_no_alloc as t
+    from faster_yoco_amd import _lib
+    dev = torch.device('cuda:0')
+    torch.cuda.set_device(dev)
+    n = 300_007
+    gen = torch.Generator(device='cpu').manual_seed(23)
+    contribs = [(torch.randn(n, generator=gen) * 1e-2).to(torch.bfloat16).to(dev) for _ in range(8)]
+    L = _lib.lib()
+    avg = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    fsum = torch.empty(n, dtype=torch.float32, device=dev)
+    sample = torch.tensor([16384.0], device=dev)
+    u, outs, flags = t._scalars(_lib, dev, sample)
+    ptrs = (ctypes.c_void_p * 8)(*[c.data_ptr() for c in contribs])
+
+    def call():
+        return L.z1_owner_sum_update_noalloc(ctypes.cast(ptrs, ctypes.c_void_p), 8, n, 0.125,
+                                             ctypes.c_void_p(avg.data_ptr()), ctypes.c_void_p(fsum.data_ptr()),
+                                             ctypes.byref(u), _lib.stream_handle(dev))
+
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, capture_error_mode='global'):      # the process's first call of the entry point
+        rc = call()
+    assert rc == 0, L.z1_strerror(rc)
+    want = t._call(None, dev, contribs, n, noalloc=False)
+    for rep in range(3):
+        for x in list(outs.values()) + [avg, fsum]:
+            x.fill_(-3.0)
+        flags.fill_(7)
+        graph.replay()
+        torch.cuda.synchronize()
+        got = {{k: v.cpu().numpy().view(np.uint32).copy() for k, v in outs.items()}}
+        got['avg'] = avg.view(torch.int16).cpu().numpy()
+        got['sum'] = fsum.cpu().numpy().view(np.uint32)
+        got['flags'] = flags.cpu().numpy()
+        for k in want:
+            assert np.array_equal(got[k], want[k]), (rep, k)
+    torch.cuda.synchronize()
+    stats0 = torch.cuda.memory_stats()
+    free0 = torch.cuda.mem_get_info()[0]
+    assert call() == 0
+    torch.cuda.synchronize()
+    stats1 = torch.cuda.memory_stats()
+    free1 = torch.cuda.mem_get_info()[0]
+    for k in ('allocation.all.allocated', 'segment.all.allocated', 'requested_bytes.all.allocated'):
+        assert stats0.get(k) == stats1.get(k), k
+    assert free0 == free1, (free0, free1)
+    print('noalloc capture-first ok')
+""")
+
+
+def test_noalloc_first_call_under_graph_capture(pkg, dev):
+    script = _CAPTURE_FIRST.format(root=ROOT, tests=os.path.join(ROOT, 'tests'))
+    res = subprocess.run([sys.executable, '-c', script], capture_output=True, text=True, timeout=110)
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-4000:]
+    assert 'noalloc capture-first ok' in res.stdout
