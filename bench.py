@@ -47,15 +47,15 @@ def traffic_file(kernel, workload):
 
 
 def load_traffic(kernel, workload):
-    """HBM bytes per launch measured by rocprofv3 --pmc (read / write request counts by size, which agree with the
-    copy-calibrated FETCH_SIZE + WRITE_SIZE), from the committed summary under profiles/, or None.  Not measured in
-    this run: counters need their own profiler runs."""
+    """The committed counter summary under profiles/ (rocprofv3 --pmc: the bytes the L2 sends to the data fabric per
+    launch, from the read / write request counts by size, which agree with the copy-calibrated FETCH_SIZE +
+    WRITE_SIZE; the MALL serves some of them, which these counters cannot see), or None.  Not measured in this run:
+    counters need their own profiler runs."""
     path = os.path.join(ROOT, traffic_file(kernel, workload))
     if not os.path.exists(path):
         return None
     with open(path) as f:
-        d = json.load(f)
-    return d.get('hbm_bytes_per_launch')
+        return json.load(f)
 
 
 def cpu_baseline(shard, cfg, ntensors, contribs, hp, step, threads):
@@ -230,8 +230,9 @@ def dropin_step_timing(dev, hp, step0, steps=20, warmup=5, world=8, rank=3):
     Algorithmic bytes: owner sum 18 B/param (8 x 2 in, 2 out) + Adam 32 B/param (BF16 g 2, p / m / v 12 in; p / m / v
     12, BF16 copy 2, FP32 gradient 4 out); the norm reads nothing (the phase sums left its partials).  Timed
     steps chain: rank 3's own slot then holds the previous step's average, the same bytes and launches.  Also timed:
-    the same with the norm read again from the gradients (ce_reduce.FUSE_NORM off, +2 B/param), and the phase sums
-    alone with phase bounds on parameter boundaries and with bounds moved off every alignment."""
+    the same with the norm read again from the gradients (ce_reduce.FUSE_NORM off, +2 B/param: its clip stage is
+    the BF16 norm pass over the 38 gradient views plus the clip chain), and the phase sums alone, on one stream, with
+    phase bounds on parameter boundaries and with bounds moved off every alignment."""
     import torch
     from faster_yoco_amd import ce_reduce, configs, layout, standins, zero1_fast
     shapes = configs.shapes('c3')
@@ -330,30 +331,42 @@ def dropin_step_timing(dev, hp, step0, steps=20, warmup=5, world=8, rank=3):
         for _ in range(warmup):
             update()
         ms, host = timed(update, steps)
-        ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(5)]
-        for e in ev:
-            update(e)
-        torch.cuda.synchronize()
         med = lambda xs: sorted(xs)[len(xs) // 2]
-        stage = {'sums_ms': med([e[0].elapsed_time(e[1]) for e in ev]),
-                 'clip_ms': med([e[1].elapsed_time(e[2]) for e in ev]),
-                 'adam_ms': med([e[2].elapsed_time(e[3]) for e in ev])}
+
+        def stages():
+            ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(5)]
+            for e in ev:
+                update(e)
+            torch.cuda.synchronize()
+            return {'sums_ms': med([e[0].elapsed_time(e[1]) for e in ev]),
+                    'clip_ms': med([e[1].elapsed_time(e[2]) for e in ev]),
+                    'adam_ms': med([e[2].elapsed_time(e[3]) for e in ev])}
+        stage = stages()
         nbytes = 50 * G
         res.update({'ms': round(ms, 4), 'host_us': round(host * 1e6, 1), 'algorithmic_bytes': nbytes,
                     'achieved_GBps': round(nbytes / (ms * 1e-3) / 1e9, 1),
                     'frac_of_peak': round(nbytes / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
-                    'stage_ms': {k: round(v, 4) for k, v in stage.items()}})
+                    'stage_ms': {k: round(v, 4) for k, v in stage.items()},
+                    'adam': {'kernel': 'adam_cast_kernel<1, 1, true>', 'bytes_per_param': 32,
+                             'GBps': round(32 * G / (stage['adam_ms'] * 1e-3) / 1e9, 1)},
+                    'sums_GBps': round(18 * G / (stage['sums_ms'] * 1e-3) / 1e9, 1)})
         ce_reduce.FUSE_NORM = False
         for _ in range(2):
             update()
         ms_u, _ = timed(update, steps)
         res['norm_read_again_ms'] = round(ms_u, 4)
+        res['norm_read_again_stage_ms'] = {k: round(v, 4) for k, v in stages().items()}
         ce_reduce.FUSE_NORM = True
-        res['sums_aligned_bounds_ms'] = round(timed(sums, steps)[0], 4)
+
+        def phases_one_stream():                                # the kernels alone: no cross-stream waits
+            for ph in range(len(ce.bounds)):
+                ce._sum(ph)
+        phases_one_stream()
+        res['sums_aligned_bounds_ms'] = round(timed(phases_one_stream, steps)[0], 4)
         odd = [0, bounds[0][1] + 1, bounds[1][1] + 3, G]        # 2- and 6-byte offsets: no common alignment
         ce.bounds = [[odd[i], odd[i + 1]] for i in range(3)]
-        sums()
-        res['sums_odd_bounds_ms'] = round(timed(sums, steps)[0], 4)
+        phases_one_stream()
+        res['sums_odd_bounds_ms'] = round(timed(phases_one_stream, steps)[0], 4)
     finally:
         ce_reduce.FUSE_NORM = True
         zero1_fast.configure(**saved)
@@ -549,6 +562,8 @@ def main():
     n = shard.numel
     step_bytes, adam_bytes, adam_bpp = algorithmic_bytes(cfg, n)
     achieved = adam_bytes / (adam_avg * 1e-3) / 1e9
+    traffic = load_traffic('adam_cast', cfg)
+    mall = traffic['mall_served_bytes_by_design'] if traffic else None
     out = {
         'metric': 'ms per optimizer step (431M-param shard); achieved HBM GB/s vs ~8 TB/s peak',
         'value': round(ms_step, 4),
@@ -576,9 +591,15 @@ def main():
                           round(sum(pre_ms) / len(pre_ms), 4)},
         'roofline': {'bound': 'hbm', 'kernel': 'adam_flat_kernel', 'achieved': round(achieved, 1),
                      'peak': PEAK_HBM_GBPS, 'unit': 'GB/s', 'frac': round(achieved / PEAK_HBM_GBPS, 4),
-                     'traffic': load_traffic('adam_cast', cfg),
+                     'traffic': traffic['l2_to_fabric_bytes_per_launch'] if traffic else None,
+                     'traffic_counted_at': 'L2 -> data fabric requests (TCC_EA0 read requests by size, 64-byte write '
+                                           'requests); MALL hits included: TCC_EA0_RDREQ_DRAM equals TCC_EA0_RDREQ'
+                                           if traffic else None,
                      'traffic_source': (traffic_file('adam_cast', cfg) + ' (rocprofv3 --pmc, committed; not measured '
-                                        'in this run)') if load_traffic('adam_cast', cfg) else None,
+                                        'in this run)') if traffic else None,
+                     'mall_served_bytes_by_design': mall,
+                     'dram_side_frac_estimate': (round((adam_bytes - mall) / (adam_avg * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4)
+                                                 if mall is not None else None),
                      'bytes_per_param': adam_bpp, 'params_per_launch': n},
         'cpu_baseline': cpu,
     }

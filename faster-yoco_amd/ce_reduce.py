@@ -30,8 +30,8 @@ def sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=None, keep_end=True):
     """OUT[e] = bf16(sum_{k=0..WORLD-1} float(x_k[e]) * scale) for e in [BASE, END), in rank order, where x_R is OUT
     itself (rank R's own gradients) and the peers' contributions sit slot-major in S ([WORLD-1, G]: peer k < R in
     slot k, k > R in slot k-1).  In place in OUT, on the current stream.  waves (float64, nullable): the range's
-    norm partials per chunk (``ops.owner_sum_waves(END - BASE)`` of them); keep_end (with waves): leave the range's
-    last 224 MB in the MALL."""
+    norm partials per chunk (``ops.owner_sum_waves(END - BASE)`` of them); keep_end: leave the range's last 224 MB
+    in the MALL."""
     ops.sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=waves, keep_end=keep_end)
 
 
@@ -84,16 +84,19 @@ def _phase_norm(ce):
 def _sum(self, ph):
     """CEReduce._sum (ce_reduce.py:178-183) on the gfx950 kernel, leaving the phase's norm partials."""
     a, b = self.bounds[ph]
-    if b > a and not FUSE_NORM:
-        sum_slots(self.staging, self.out, self.G, a, b, self.rank, 1.0 / self.world, self.world)
-    elif b > a:
-        pn = _phase_norm(self)
-        o = pn.offset[ph]
-        # only the end of out is read first by the update (FusedAdamCast walks its gradients from the highest
-        # address down); a phase summed during the backward would only push it out of the MALL
-        sum_slots(self.staging, self.out, self.G, a, b, self.rank, 1.0 / self.world, self.world,
-                  waves=pn.waves[o:o + pn.count[ph]], keep_end=b == self.G)
-        pn.summed[ph] = True
+    if b <= a:
+        return
+    # only the end of out is read first by the update (FusedAdamCast walks its gradients from the highest address
+    # down); a phase summed during the backward would only push it out of the MALL
+    keep = b == self.G
+    if not FUSE_NORM:
+        sum_slots(self.staging, self.out, self.G, a, b, self.rank, 1.0 / self.world, self.world, keep_end=keep)
+        return
+    pn = _phase_norm(self)
+    o = pn.offset[ph]
+    sum_slots(self.staging, self.out, self.G, a, b, self.rank, 1.0 / self.world, self.world,
+              waves=pn.waves[o:o + pn.count[ph]], keep_end=keep)
+    pn.summed[ph] = True
 
 
 def take_norm_partials(grads):

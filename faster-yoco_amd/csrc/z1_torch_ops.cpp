@@ -566,8 +566,8 @@ void owner_sum_update_(TensorList contribs, const Tensor& out, const Tensor& wor
 // The owner sum in the reference's staging layout (yoco/models/decoder/ce_reduce.py:59-74): the contribution of
 // peer k < rank in slot k of `staging`, of k > rank in slot k - 1, rank's own in `out`, summed in rank order into
 // out[base:end].  With `waves` (at least z1_owner_sum_waves(end - base) float64), the norm of the range's average
-// is left there per chunk (z1_owner_sum_bf16_waves), for reduce_waves_; keep_end as z1_owner_sum_bf16_waves takes it
-// (without waves the range's end is always kept).
+// is left there per chunk (z1_owner_sum_bf16_waves), for reduce_waves_; keep_end as z1_owner_sum_bf16_waves takes
+// it.
 void sum_slots_(const Tensor& staging, const Tensor& out, int64_t G, int64_t base, int64_t end, int64_t rank,
                 double scale, int64_t world, const OptTensor& waves, bool keep_end) {
     TORCH_CHECK(staging.defined() && staging.is_cuda() && staging.scalar_type() == at::kBFloat16 &&
@@ -590,13 +590,9 @@ void sum_slots_(const Tensor& staging, const Tensor& out, int64_t G, int64_t bas
     for (int64_t k = 0; k < world; ++k)
         ptrs[k] = k < rank ? s0 + k * G + base : (k == rank ? o0 + base : s0 + (k - 1) * G + base);
     OnDevice on(out);
-    if (wp)
-        check_rc(api().owner_sum_bf16_waves(ptrs, static_cast<int>(world), end - base, static_cast<float>(scale),
-                                            o0 + base, nullptr, wp, keep_end ? 1 : 0, on.stream),
-                 "z1_owner_sum_bf16_waves");
-    else
-        check_rc(api().owner_sum_bf16(ptrs, static_cast<int>(world), end - base, static_cast<float>(scale),
-                                      o0 + base, nullptr, nullptr, on.stream), "z1_owner_sum_bf16");
+    check_rc(api().owner_sum_bf16_waves(ptrs, static_cast<int>(world), end - base, static_cast<float>(scale),
+                                        o0 + base, nullptr, wp, keep_end ? 1 : 0, on.stream),
+             "z1_owner_sum_bf16_waves");
 }
 
 // The fixed-order reduction of per-chunk norm partials (the first m of `waves`) into the norm's partials.

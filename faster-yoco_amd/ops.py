@@ -1,7 +1,10 @@
 """The public operations of the path, each a call of a ``torch.ops.yoco_z1`` operator (C++ over the C ABI, loaded by
-``library.py``).  Every call enqueues on torch's current stream of the tensors' device, performs no host synchronisation
-and allocates nothing (tables are made once, at set-up; a Python-number factor and a device output may be mixed as
-the reference's fairseq surface mixes them).
+``library.py``).  Every call enqueues on torch's current stream of the tensors' device and performs no host
+synchronisation.  The calls allocate no device memory (tables and workspaces are made at set-up, by
+``Table`` / ``TableCache`` / ``norm_workspace``), with one exception: a factor given as a tensor to be read but not
+written (``factor_out`` None or another tensor) is copied first -- into ``factor_out`` when one is given, else into a
+new tensor -- because the operators write the clipped factor over the one they read.  A Python-number factor and a
+device output may be mixed as the reference's fairseq surface mixes them.
 
 ``table`` arguments are ``Table`` objects (``kernels.Table``); without explicit tensors an operation runs on the
 tensors the table was made with (``Table.bound``).
@@ -147,7 +150,7 @@ def owner_sum_update(contribs, out, scale, workspace, out_sum=None, sample_size=
 def sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=None, keep_end=True):
     """The owner sum in the reference's staging layout, in place (yoco/models/decoder/ce_reduce.py:59-74).  waves
     (float64, at least owner_sum_waves(END - BASE)): the range's norm partials per chunk, for reduce_waves.
-    keep_end (with waves): leave the range's last 224 MB in the MALL for the pass that reads them next."""
+    keep_end: leave the range's last 224 MB in the MALL for the pass that reads them next."""
     _OPS.sum_slots_(S, OUT, int(G), int(BASE), int(END), int(R), f32(scale), int(WORLD), waves, bool(keep_end))
 
 

@@ -106,10 +106,24 @@ class _Plan:
         if FUSED_ADAM and hasattr(oss.optim, 'multi_tensor_adam'):
             self.fused = FusedAdamCast({b.data_ptr(): view for _, b, view in self.mine if view.is_contiguous()})
             oss.optim.multi_tensor_adam = self.fused
+        elif hasattr(oss.optim, 'multi_tensor_adam'):
+            # without YOCO_FUSED_ADAM the reference leaves FusedAdamV2 on apex's amp_C.multi_tensor_adam
+            # (zero1_fast.py:125-129 replace it only with the switch): here the same call, amp_C's signature, runs
+            # this build's Adam without BF16 destinations, and the step's casts write every BF16 copy as there
+            oss.optim.multi_tensor_adam = FusedAdamCast({})
         if CE_ALLGATHER and self.placed:
             raise RuntimeError('zero1_fast: YOCO_CE_ALLGATHER (CUDA IPC copy-engine exchange) is not part of this build')
         self.partials = None
         self.norm_tables = ops.TableCache(4)
+        self.scalars = None                           # device scalars of clip / step: n_r, the factor (see _scalar)
+
+    def scalar(self, k, dev):
+        """The plan's k-th 1-element fp32 device scalar (0: the owner's norm n_r, 1: the clipped factor when fairseq's
+        factor is a Python number, 2: that number for the step), made once: a step allocates nothing but the
+        grad_norm tensor clip_grad_norm returns (a new one each time, as the reference's is)."""
+        if self.scalars is None or self.scalars.device != dev:
+            self.scalars = torch.zeros(3, dtype=torch.float32, device=dev)
+        return self.scalars[k:k + 1]
 
     def exchange(self):
         """Every owner's BF16 segment to every rank (zero1_fast.py:224-231): one all-gather over the flat buffer, or
@@ -139,13 +153,16 @@ def _plan(opt):
     return plan or None
 
 
-def _device_factor(factor, dev):
-    """fairseq's _multiply_factor as a 1-element fp32 tensor on `dev` (the same tensor when it is one)."""
+def _device_factor(factor, dev, buf=None):
+    """fairseq's _multiply_factor as a 1-element fp32 tensor on `dev`: the same tensor when it is one; a Python number
+    is filled into `buf` (a fill kernel, no host copy) or a new tensor."""
     if torch.is_tensor(factor):
         if factor.dtype == torch.float32 and factor.device == dev and factor.numel() == 1:
             return factor
         return factor.to(device=dev, dtype=torch.float32).reshape(1)
-    return torch.full((1,), float(factor), dtype=torch.float32, device=dev)     # a fill kernel, no host copy
+    if buf is not None:
+        return buf.fill_(float(factor))
+    return torch.full((1,), float(factor), dtype=torch.float32, device=dev)
 
 
 def clip_grad_norm(self, max_norm, aggregate_norm_fn=None):
@@ -171,8 +188,8 @@ def clip_grad_norm(self, max_norm, aggregate_norm_fn=None):
     factor = self._multiply_factor
     if torch.is_tensor(factor):
         factor = _device_factor(factor, dev)
-    out = factor if torch.is_tensor(factor) else torch.empty(1, dtype=torch.float32, device=dev)
-    grad_norm = torch.empty(1, dtype=torch.float32, device=dev)
+    out = factor if torch.is_tensor(factor) else plan.scalar(1, dev)
+    grad_norm = torch.empty(1, dtype=torch.float32, device=dev)        # returned: a new tensor per call
     clip = float(max_norm) if max_norm > 0.0 else 0.0
     # the owned gradients are the average CEReduce's phase sums wrote: their norm partials are already there
     fused = ce_reduce.take_norm_partials(grads) if REDUCE_OWNER else None
@@ -198,7 +215,7 @@ def clip_grad_norm(self, max_norm, aggregate_norm_fn=None):
             ops.grad_sumsq(table, plan.partials, g=grads)
         else:
             plan.partials.zero_()
-        n_r = torch.empty(1, dtype=torch.float32, device=dev)
+        n_r = plan.scalar(0, dev)
         ops.norm_clip(plan.partials, norm_out=n_r)              # the owner's (or every rank's) fp32 norm
         if REDUCE_OWNER:
             sq = n_r ** 2                                       # owners' squared norms summed over the group
@@ -239,7 +256,8 @@ def step(self, closure=None, groups=None):
         if b.grad is None:
             b.grad = torch.zeros_like(b)
     if plan.mine:
-        f1 = _device_factor(self._multiply_factor, plan.mine[0][1].device)
+        dev = plan.mine[0][1].device
+        f1 = _device_factor(self._multiply_factor, dev, plan.scalar(2, dev))
         folded = {}
         if plan.fused is not None:
             folded = {b.data_ptr(): a.grad for a, b, _ in plan.mine

@@ -120,8 +120,8 @@ int64_t z1_owner_sum_workspace(int64_t n);
  * keeps the vector path); this count covers every grid. */
 int64_t z1_owner_sum_waves(int64_t n);
 
-/* z1_owner_sum_bf16 with the fused norm left per chunk: waves (z1_owner_sum_waves(n) doubles) receives each chunk's
- * FP64 sum of squares of the BF16 average (a fixed decomposition; nothing is reduced).  For a caller that sums a
+/* z1_owner_sum_bf16 with the fused norm left per chunk: waves (z1_owner_sum_waves(n) doubles; nullable: no norm)
+ * receives each chunk's FP64 sum of squares of the BF16 average (a fixed decomposition; nothing is reduced).  For a caller that sums a
  * gradient buffer one range at a time -- CEReduce._sum, once per backward phase
  * (yoco/models/decoder/ce_reduce.py:178-183,205-209,227) -- and wants the norm of the whole buffer without reading
  * it again, as yoco/tasks/zero1_fast.py:150 does: the ranges' partials, side by side in one array, go to

@@ -32,12 +32,21 @@ def test_algorithmic_bytes():
 
 
 def test_committed_traffic_summaries_parse():
-    for kernel, workload in (('adam_cast', 'c2'), ('adam_cast', 'c3'), ('sumsq', 'c2'), ('owner_sum', 'c3')):
+    """Every committed counter summary states what it counts (L2 -> fabric requests), the bytes the MALL serves by
+    design, and measured / algorithmic bytes consistent with its own fields."""
+    n = 430_662_912
+    alg = {('adam_cast', 'c2'): 30 * n, ('adam_cast', 'c3'): 28 * n, ('sumsq', 'c2'): 4 * n,
+           ('owner_sum', 'c3'): 18 * n, ('adam_cast', 'dropin'): 32 * n}
+    for (kernel, workload), bytes_ in alg.items():
         t = bench.load_traffic(kernel, workload)
-        assert t is None or t > 0, (kernel, workload)
-    with open(os.path.join(ROOT, 'profiles', 'adam_cast_c2_traffic.json')) as f:
-        d = json.load(f)
-    assert abs(d['hbm_bytes_per_launch'] / (30 * 430_662_912) - 1) < 0.01
+        assert t is not None, (kernel, workload)
+        assert 'MALL' in t['counted_at'] and t['mall_served_bytes_by_design'] >= 0
+        total = t['l2_to_fabric_read_bytes'] + t['l2_to_fabric_write_bytes']
+        assert total == t['l2_to_fabric_bytes_per_launch']
+        assert t['algorithmic_read_bytes'] + t['algorithmic_write_bytes'] == bytes_
+        assert abs(total / bytes_ - t['measured_over_algorithmic']) < 1e-4
+        assert 1.0 <= t['measured_over_algorithmic'] < 1.01, (kernel, workload)
+        assert t['dram_bytes_per_launch_estimate'] == total - t['mall_served_bytes_by_design']
 
 
 def test_config_sizes(pkg):

@@ -151,7 +151,8 @@ def expected_update(params, grads16, state, step, factor0, max_norm, reduce_owne
     dict(ONE_PASS=True, SCALE_KERNEL=True, FOLD_SCALE=False),
     dict(ONE_PASS=False, SCALE_KERNEL=False, FOLD_SCALE=False),
     dict(ONE_PASS=True, SCALE_KERNEL=True, FOLD_SCALE=True, ALLGATHER=True),
-], ids=['fold', 'scale_kernel', 'foreach', 'allgather_buffer'])
+    dict(ONE_PASS=True, SCALE_KERNEL=True, FOLD_SCALE=False, FUSED_ADAM=False),
+], ids=['fold', 'scale_kernel', 'foreach', 'allgather_buffer', 'no_fused_adam'])
 @pytest.mark.parametrize('reduce_owner', [False, True], ids=['all_grads', 'reduce_owner'])
 def test_zero1_fast_trainer_sequence(pkg, dev, switches, reduce_owner):
     from faster_yoco_amd import zero1_fast
@@ -192,6 +193,11 @@ def test_zero1_fast_trainer_sequence(pkg, dev, switches, reduce_owner):
         opt.step()
         torch.cuda.synchronize()
         assert opt._multiply_factor == 1.0
+        if not sw['FUSED_ADAM']:
+            # amp_C's multi_tensor_adam replaced by this build's Adam without BF16 destinations (the step's casts
+            # write the BF16 copies)
+            from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+            assert isinstance(oss.optim.multi_tensor_adam, FusedAdamCast) and oss.optim.multi_tensor_adam.dest == {}
         if not sw.get('FOLD_SCALE'):
             # the masters' FP32 gradients are written as the reference writes them: fp32(float(g16) * factor)
             for i, p32 in enumerate(opt.fp32_params):
@@ -420,6 +426,7 @@ def test_ce_reduce_phase_norm_feeds_clip_grad_norm(pkg, dev, monkeypatch):
                 params[1].grad = params[1].grad.clone()          # no longer a view of out
             grads16 = [avg[o - n:o] for o, n in zip(ends, numels)]
             before = used['pass']
+            allocs = torch.cuda.memory_stats()['allocation.all.allocated']
             gn = opt.clip_grad_norm(max_norm)
             assert (used['pass'] == before) == (fused is True), step
             fac = float(opt._multiply_factor.item())
@@ -430,6 +437,8 @@ def test_ce_reduce_phase_norm_feeds_clip_grad_norm(pkg, dev, monkeypatch):
                 assert np.float32(fac) == exp_fac, step
             opt.step()
             torch.cuda.synchronize()
+            if step == 2:                      # a recurring update allocates only the grad_norm it returns
+                assert torch.cuda.memory_stats()['allocation.all.allocated'] - allocs == 1
             for i, p in enumerate(params):
                 po, mo, vo, p16 = oracle.adam_cast(grads16[i], *state[i], step=step, factor=fac, **HP)
                 st = opt.fp32_optimizer.optimizer.optim.state[opt.fp32_params[i]]
