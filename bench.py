@@ -15,6 +15,8 @@ With c2 or c3 the line also carries ``dropin_step``: the update at C3's shape th
 (CEReduce._sum per phase, zero1_fast.clip_grad_norm, zero1_fast.step -> FusedAdamCast), timed after the main steps.
 """
 import argparse
+import contextlib
+import gc
 import json
 import math
 import os
@@ -33,6 +35,19 @@ WORKLOADS = {
            'fp32 tensors (the largest shard), step 1000',
     'c4r': 'C4R unsharded YOCO-3B on its 240 real tensors: 3,445,303,296 params, step 1000',
 }
+
+
+@contextlib.contextmanager
+def gc_paused():
+    """Python's cyclic garbage collector held off for a timed loop, as timeit holds it off: a collection pass that
+    lands in the loop stops the host for tens of milliseconds, long enough for the GPU to run dry and idle."""
+    was = gc.isenabled()
+    gc.disable()
+    try:
+        yield
+    finally:
+        if was:
+            gc.enable()
 
 
 def algorithmic_bytes(cfg, n):
@@ -145,11 +160,12 @@ def glue_timing(opt, hp, iters=200):
         for _ in range(20):
             fn()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(iters):
-            fn()
-        torch.cuda.synchronize()
-        out[name] = round((time.perf_counter() - t0) * 1e6 / iters, 1)
+        with gc_paused():
+            t0 = time.perf_counter()
+            for _ in range(iters):
+                fn()
+            torch.cuda.synchronize()
+            out[name] = round((time.perf_counter() - t0) * 1e6 / iters, 1)
     return out
 
 
@@ -199,13 +215,14 @@ def dropin_timing(dev, hp, step, reps=10):
             call()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        e0.record()
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            call()
-        host = time.perf_counter() - t0
-        e1.record()
-        torch.cuda.synchronize()
+        with gc_paused():
+            e0.record()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                call()
+            host = time.perf_counter() - t0
+            e1.record()
+            torch.cuda.synchronize()
         out[name] = round(e0.elapsed_time(e1) / reps, 4)
         out[name.replace('_ms', '_host_us')] = round(host / reps * 1e6, 1)
         fa.cast.clear()
@@ -317,13 +334,14 @@ def dropin_step_timing(dev, hp, step0, steps=20, warmup=5, world=8, rank=3):
     def timed(fn, k):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        e0.record()
-        t0 = time.perf_counter()
-        for _ in range(k):
-            fn()
-        host = time.perf_counter() - t0
-        e1.record()
-        torch.cuda.synchronize()
+        with gc_paused():
+            e0.record()
+            t0 = time.perf_counter()
+            for _ in range(k):
+                fn()
+            host = time.perf_counter() - t0
+            e1.record()
+            torch.cuda.synchronize()
         return e0.elapsed_time(e1) / k, host / k
 
     res = {'tensors': len(shapes), 'params': G, 'world': world, 'rank': rank, 'phases': len(ce.bounds)}
@@ -406,11 +424,12 @@ def pipeline_timing(shard, opt, k, reps=10):
             fn()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
+        with gc_paused():
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
         out[name] = round(e0.elapsed_time(e1) / reps, 4)
     return out
 
@@ -437,11 +456,12 @@ def embedding_timing(dev, reps=20):
             fn()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
-        e0.record()
-        for _ in range(reps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
+        with gc_paused():
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
         return round(e0.elapsed_time(e1) / reps, 4)
 
     res = {}
@@ -547,12 +567,13 @@ def main():
     every = max(1, args.steps // 5)
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(0, args.steps, every)]
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        one_step(events[i // every] if i % every == 0 else None)
-    enqueued = time.perf_counter() - t0                 # the host's share: every launch of the K steps enqueued
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    with gc_paused():
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            one_step(events[i // every] if i % every == 0 else None)
+        enqueued = time.perf_counter() - t0             # the host's share: every launch of the K steps enqueued
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
 
     ms_step = wall * 1e3 / args.steps
     adam_ms = [e[1].elapsed_time(e[2]) for e in events]
