@@ -13,6 +13,7 @@ Inputs are synthetic.  GPU inputs come from torch's seeded generator on the devi
 inputs come from NumPy's seeded PCG64 on the host (``host_inputs``) so the oracle sees the same arrays.
 """
 import math
+import os
 
 import numpy as np
 import torch
@@ -176,6 +177,68 @@ def host_inputs(n, name='c1', seed=0):
             u = c.view(np.uint32).astype(np.uint64)
             contribs.append(((u + 0x7fff + ((u >> 16) & 1)) >> 16).astype(np.uint16))
         out['contribs'] = contribs
+    return out
+
+
+_BASELINE_FIELDS = {'p': 0, 'm': 1, 'v': 2, 'g': 3, 'outliers': 4}      # contribution r: 16 + r
+
+
+def baseline_inputs(name, seed=0, pieces=64, threads=None):
+    """Full-size NumPy inputs of config `name` with BASELINE.json's distributions -- p ~ N(0, 0.02), the config's
+    m ~ N(0, m_std), v = |N(0, v_std)|, g ~ N(0, g_std) (c5: Student-t(2) x 1e-3 from the closed form of SURVEY
+    §8(d), exactly round(1e-3 n) entries set to +-1e4; c3: eight BF16 contributions ~ N(0, 1e-4), no g) -- as float32
+    (contributions as uint16 bf16 bits).  Each field is cut into `pieces` fixed pieces, each drawn from its own PCG64
+    stream seeded by (seed, field, piece), so the bits do not depend on `threads` (NumPy releases the GIL while it
+    fills and computes, so the pieces run in parallel)."""
+    from concurrent.futures import ThreadPoolExecutor
+    cfg = CONFIGS[name]
+    n = numel(name)
+    bounds = [n * k // pieces for k in range(pieces + 1)]
+
+    def rng(fid, k):
+        return np.random.Generator(np.random.PCG64(np.random.SeedSequence([seed, fid, k])))
+
+    def normal(fid, std, out, absolute=False):
+        def piece(k):
+            lo, hi = bounds[k], bounds[k + 1]
+            x = rng(fid, k).standard_normal(hi - lo, dtype=np.float32)
+            x *= np.float32(std)
+            out[lo:hi] = np.abs(x) if absolute else x
+        return [(piece, k) for k in range(pieces)]
+
+    def student(out):
+        def piece(k):
+            lo, hi = bounds[k], bounds[k + 1]
+            u = (rng(_BASELINE_FIELDS['g'], k).integers(0, 1 << 24, hi - lo).astype(np.float64) + 0.5) / float(1 << 24)
+            out[lo:hi] = ((2.0 * u - 1.0) / np.sqrt(2.0 * u * (1.0 - u)) * cfg['g_std']).astype(np.float32)
+        return [(piece, k) for k in range(pieces)]
+
+    def bf16(fid, std, out):
+        def piece(k):
+            lo, hi = bounds[k], bounds[k + 1]
+            x = rng(fid, k).standard_normal(hi - lo, dtype=np.float32)
+            x *= np.float32(std)
+            u = x.view(np.uint32)
+            out[lo:hi] = ((u + np.uint32(0x7fff) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+        return [(piece, k) for k in range(pieces)]
+
+    out = {f: np.empty(n, np.float32) for f in ('p', 'm', 'v')}
+    jobs = normal(0, 0.02, out['p']) + normal(1, cfg['m_std'], out['m']) + normal(2, cfg['v_std'], out['v'], True)
+    if cfg['grad'] == 'owner8':
+        out['contribs'] = [np.empty(n, np.uint16) for _ in range(8)]
+        for r in range(8):
+            jobs += bf16(16 + r, cfg['g_std'], out['contribs'][r])
+    else:
+        out['g'] = np.empty(n, np.float32)
+        jobs += student(out['g']) if cfg['grad'] == 'student_t' else normal(3, cfg['g_std'], out['g'])
+    with ThreadPoolExecutor(max_workers=threads or min(16, os.cpu_count() or 1)) as ex:
+        for f in [ex.submit(fn, k) for fn, k in jobs]:
+            f.result()
+    if cfg['grad'] == 'student_t':
+        k = int(round(1e-3 * n))
+        r = rng(_BASELINE_FIELDS['outliers'], 0)
+        idx = r.choice(n, size=k, replace=False)
+        out['g'][idx] = np.where(r.integers(0, 2, k) == 1, np.float32(1e4), np.float32(-1e4))
     return out
 
 

@@ -2,6 +2,7 @@
 
     python tests/golden/make_fixtures.py            # the small fixtures and the C1 digest (seconds)
     python tests/golden/make_fixtures.py --large    # large_digests.json: C2, C3, C5, C4 at full size (minutes)
+    python tests/golden/make_fixtures.py --baseline # baseline_digests.json: C2, C3, C5 on BASELINE's distributions
 
 Each fixture is an .npz (no pickles) holding the inputs of a small update and the CPU oracle's outputs:
 owner-sum average (c3), the norm n_r, grad_norm, the clipped factor, and the Adam outputs p, m, v, p16 computed
@@ -148,7 +149,45 @@ def large_digest(name, chunk=1 << 25):
             'sha256': {k: h.hexdigest() for k, h in hs.items()}, 'input_prefix_sha256': prefix}
 
 
+def baseline_digest(name):
+    """The full-size update of config `name` (c2, c3, c5) on BASELINE.json's own distributions
+    (configs.baseline_inputs, seed 0: normals, Student-t with outliers, eight BF16 contributions), through the
+    oracle: the norm (c3: of the rank-order BF16 average) -> clip at 1.0 -> Adam mode 1 at the config's step with
+    the clipped factor; the bits of norm / grad_norm / factor and sha256 of p, m, v, the BF16 copy (and the BF16
+    average for c3), plus sha256 of the first PREFIX elements of every input."""
+    import __graft_entry__
+    __graft_entry__.package()
+    from faster_yoco_amd import configs
+    x = configs.baseline_inputs(name, seed=0)
+    step = configs.CONFIGS[name]['step']
+    g = oracle.owner_sum(x['contribs']) if name == 'c3' else x['g']
+    prefix = {f: sha256(x[f][:PREFIX]) for f in ('p', 'm', 'v')}
+    if name == 'c3':
+        prefix.update({f'c{r}': sha256(c[:PREFIX]) for r, c in enumerate(x['contribs'])})
+    else:
+        prefix['g'] = sha256(x['g'][:PREFIX])
+    nr, gn, fac = oracle.norm_clip(oracle.sumsq(g), 1.0, MAX_NORM)
+    po, mo, vo, p16 = oracle.adam_cast(g, x['p'], x['m'], x['v'], step=step, mode=1, factor=fac, **HP)
+    digests = {'p': sha256(po), 'm': sha256(mo), 'v': sha256(vo), 'p16': sha256(p16)}
+    if name == 'c3':
+        digests['avg16'] = sha256(g)
+    return {'config': name, 'params': int(g.size), 'step': step, 'mode': 1, 'hparams': HP, 'max_norm': MAX_NORM,
+            'inputs': 'faster_yoco_amd.configs.baseline_inputs(name, seed=0)', 'prefix_elements': PREFIX,
+            'norm_bits': f32_hex(nr), 'grad_norm_bits': f32_hex(gn), 'factor_bits': f32_hex(fac),
+            'sha256': digests, 'input_prefix_sha256': prefix}
+
+
 def main():
+    if '--baseline' in sys.argv[1:]:
+        d = {}
+        for name in ('c2', 'c3', 'c5'):
+            d[name] = baseline_digest(name)
+            print('baseline digest of', name, 'done', flush=True)
+        with open(os.path.join(HERE, 'baseline_digests.json'), 'w') as f:
+            json.dump(d, f, indent=1)
+            f.write('\n')
+        print('baseline digests written to', HERE)
+        return
     if '--large' in sys.argv[1:]:
         # --large [name ...]: (re)computes the named configs (default: all) and keeps the others' entries
         import __graft_entry__
