@@ -1,0 +1,111 @@
+"""Host-side logic of the drop-in seams, on the CPU (nothing is launched): the plan zero1_fast makes for an
+OSS-sharded fairseq optimizer -- which multi_tensor_adam it installs with and without YOCO_FUSED_ADAM
+(yoco/tasks/zero1_fast.py:125-129) -- and the bookkeeping CEReduce's phase sums leave for clip_grad_norm: one slice of
+partials per phase (yoco/models/decoder/ce_reduce.py:122-140 lays the phases out in the owner's gradient), whether the
+phases tile the gradient, and when clip_grad_norm may take the partials."""
+import torch
+
+from faster_yoco_amd import standins
+
+
+def cpu_params(shapes):
+    return [torch.nn.Parameter(torch.zeros(s, dtype=torch.bfloat16)) for s in shapes]
+
+
+def make_opt(zero1_fast, shapes):
+    class Mixin(standins.FakeMixin):
+        pass
+
+    zero1_fast._ORIG.clear()
+    assert zero1_fast.install(Mixin)
+
+    class Opt(Mixin, standins.FakeFP16Optimizer):
+        pass
+
+    return Opt(cpu_params(shapes))
+
+
+def test_plan_installs_this_builds_adam_with_and_without_the_switch(pkg):
+    from faster_yoco_amd import zero1_fast
+    from faster_yoco_amd.fused_adam_cast import FusedAdamCast
+    shapes = [(8, 4), (16,), (3, 5)]
+    try:
+        zero1_fast.configure(ENABLED=True, FUSED_ADAM=True, ALLGATHER=False, PARAM_VIEWS=False, REDUCE_OWNER=False)
+        opt = make_opt(zero1_fast, shapes)
+        plan = zero1_fast._plan(opt)
+        mta = opt.fp32_optimizer.optimizer.optim.multi_tensor_adam
+        assert plan.fused is mta and isinstance(mta, FusedAdamCast)
+        assert set(mta.dest) == {p.data_ptr() for p in opt.fp32_params}       # every owned master has a copy
+        zero1_fast.configure(FUSED_ADAM=False)
+        opt = make_opt(zero1_fast, shapes)
+        plan = zero1_fast._plan(opt)
+        mta = opt.fp32_optimizer.optimizer.optim.multi_tensor_adam
+        assert plan.fused is None                       # no folding: the scale pass runs as in the reference
+        assert isinstance(mta, FusedAdamCast) and mta.dest == {}                # amp_C's replacement, no copies
+        s0, s1 = plan.scalar(0, torch.device('cpu')), plan.scalar(1, torch.device('cpu'))
+        assert s0.numel() == s1.numel() == 1 and s0.data_ptr() != s1.data_ptr()
+        assert plan.scalar(0, torch.device('cpu')).data_ptr() == s0.data_ptr()  # made once
+    finally:
+        zero1_fast.configure(ENABLED=False, FUSED_ADAM=False)
+        zero1_fast._ORIG.clear()
+
+
+def test_phase_norm_slices_and_tiling(pkg):
+    from faster_yoco_amd import ce_reduce, ops
+    G = 10_000
+    out = torch.zeros(G, dtype=torch.bfloat16)
+    staging = torch.zeros(7 * G, dtype=torch.bfloat16)
+    bounds = [[0, 4099], [4099, 4099], [4099, 7001], [7001, G]]
+    ce = standins.FakeCEReduce(staging, out, G, bounds, 3, 8)
+    pn = ce_reduce.PhaseNorm(ce)
+    want = [ops.owner_sum_waves(b - a) if b > a else 0 for a, b in bounds]
+    assert pn.count == want and pn.offset == [0, want[0], want[0], want[0] + want[2]] and pn.m == sum(want)
+    assert pn.waves.numel() == pn.m and pn.waves.dtype == torch.float64
+    assert pn.tiles and not pn.ready()
+    pn.summed = [True, False, True, True]                # the empty phase needs no sum
+    assert pn.ready()
+    assert pn.matches(ce)
+    ce.bounds = [[0, 4099], [4100, G]]                   # a gap: the phases no longer tile out
+    assert not pn.matches(ce)                           # made again at the next phase sum
+    gap = ce_reduce.PhaseNorm(ce)
+    assert not gap.tiles and gap.matches(ce)
+    gap.summed = [True, True]
+    assert not gap.ready()
+
+
+def test_take_norm_partials_needs_gradients_that_are_the_views_of_out(pkg):
+    """CPU gradients never qualify (the partials are device memory), whatever their layout; and with FUSE_NORM off
+    nothing is taken."""
+    from faster_yoco_amd import ce_reduce
+    out = torch.zeros(64, dtype=torch.bfloat16)
+    assert ce_reduce.take_norm_partials([out[:32], out[32:]]) is None
+    assert ce_reduce.take_norm_partials([]) is None
+    old = ce_reduce.FUSE_NORM
+    try:
+        ce_reduce.FUSE_NORM = False
+        assert ce_reduce.take_norm_partials([out]) is None
+    finally:
+        ce_reduce.FUSE_NORM = old
+
+
+def test_fused_adam_cast_orders_a_tables_rows_by_gradient_address(pkg):
+    """FusedAdamCast builds each table with its rows sorted by the gradients' addresses (the launch then starts at
+    the highest one, what the pass before it wrote last) and maps the call's lists to that order."""
+    from faster_yoco_amd import fused_adam_cast
+    made = []
+
+    class FakeCache:
+        def get(self, rows, device):
+            made.append([r[0].data_ptr() for r in rows])
+            return object()
+
+    fa = fused_adam_cast.FusedAdamCast({})
+    fa._tables = FakeCache()
+    flat = torch.zeros(300)
+    g = [flat[200:300], flat[0:100], flat[100:200]]          # gradients in descending-then-ascending order
+    p = [torch.zeros(100) for _ in g]
+    key = tuple((t.data_ptr(), t.numel()) for t in p)
+    groups, written = fa._plan(key, None, [g, p, [torch.zeros(100) for _ in g], [torch.zeros(100) for _ in g]], None)
+    assert made == [sorted(t.data_ptr() for t in g)]
+    (folded, idx, _, p16), = groups
+    assert not folded and idx == (1, 2, 0) and p16 == [] and written == ()
