@@ -816,7 +816,10 @@ struct z1_table {
     int64_t nchunks;
     std::vector<Row> host_rows;   // host copy of the device rows' pointers, kept by rebind / set_grads
     int host_valid;       // 0 once a rebind / set_grads launch failed: the device rows may differ from host_rows
-    int rows_failed;      // a rebind / set_grads launch failed: launches are refused until a z1_table_rebind succeeds
+    int g_failed;         // a rebind / set_grads launch failed: the gradient column may be half rewritten; every
+                          // launch is refused until a z1_table_set_grads or z1_table_rebind succeeds
+    int pmv_failed;       // a rebind launch failed: p, m, v, p16 may be half rewritten; Adam is refused until a
+                          // z1_table_rebind succeeds (the norm reads only the gradients)
     int gout_failed;      // a set_grad_out launch failed: Adam is refused until a z1_table_set_grad_out succeeds
     int contig;           // the device rows tile one allocation per stream in order, without gaps (see set_contig)
     Row whole;            // when contig: the first row's pointers, n = numel, the vector flags of the whole
@@ -1021,7 +1024,7 @@ int z1_table_rebind(z1_table* table, const z1_tensor* rows, int nrows, void* str
             rc = launch_status();
             if (rc) {
                 table->host_valid = 0;
-                table->rows_failed = 1;
+                table->g_failed = table->pmv_failed = 1;
                 return rc;
             }
             b.count = 0;
@@ -1032,12 +1035,12 @@ int z1_table_rebind(z1_table* table, const z1_tensor* rows, int nrows, void* str
         rc = launch_status();
         if (rc) {
             table->host_valid = 0;
-            table->rows_failed = 1;
+            table->g_failed = table->pmv_failed = 1;
             return rc;
         }
     }
     table->host_valid = 1;                             // every row's pointers as host_rows now holds them
-    table->rows_failed = 0;
+    table->g_failed = table->pmv_failed = 0;
     set_contig(table);
     return Z1_OK;
 }
@@ -1068,7 +1071,7 @@ int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* s
             rc = launch_status();
             if (rc) {
                 table->host_valid = 0;
-                table->rows_failed = 1;
+                table->g_failed = 1;
                 return rc;
             }
             b.count = 0;
@@ -1079,10 +1082,11 @@ int z1_table_set_grads(z1_table* table, const void* const* g, int nrows, void* s
         rc = launch_status();
         if (rc) {
             table->host_valid = 0;
-            table->rows_failed = 1;
+            table->g_failed = 1;
             return rc;
         }
     }
+    table->g_failed = 0;                               // every row's gradient rewritten
     set_contig(table);
     return Z1_OK;
 }
@@ -1142,7 +1146,7 @@ static int launch_sumsq(const z1_table* table, double* partials, const z1_update
     int dev = 0;
     int rc = check_table_device(table, &dev);
     if (rc) return rc;
-    if (table->rows_failed) return Z1_E_STATE;
+    if (table->g_failed) return Z1_E_STATE;
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t kf = keep_from(table);
     if (table->g_dtype == Z1_F32)
@@ -1219,7 +1223,7 @@ static int adam_launch(const z1_table* table, int64_t chunk_begin, int64_t chunk
     int dev = 0;
     int rc = check_table_device(table, &dev);
     if (rc) return rc;
-    if (table->rows_failed || table->gout_failed) return Z1_E_STATE;
+    if (table->g_failed || table->pmv_failed || table->gout_failed) return Z1_E_STATE;
     if (chunk_end <= chunk_begin) return Z1_OK;
     AdamK k;
     k.lr = lr;

@@ -37,8 +37,9 @@ enum {
     Z1_E_DEVICE = -7,      /* table used on a device other than the one it was created on */
     Z1_E_NOALLOC_MAX = -8, /* input larger than the no-allocation entry point's fixed scratch */
     Z1_E_STATE = -9,       /* a binding launch on the table failed (its device rows may be half rewritten): launches
-                              over it are refused until z1_table_rebind (rows) / z1_table_set_grad_out (outputs)
-                              succeeds */
+                              that read what it was rewriting are refused until it is bound again -- the gradients
+                              by z1_table_set_grads or z1_table_rebind, the other columns by z1_table_rebind, the
+                              FP32 gradient outputs by z1_table_set_grad_out */
 };
 
 enum { Z1_F32 = 0, Z1_BF16 = 1 };           /* gradient dtype codes */
