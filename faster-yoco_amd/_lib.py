@@ -46,7 +46,7 @@ SIGNATURES = {
     'z1_owner_sum_bf16': ([_P, _I, _I64, _F, _P, _P, _P, _P], _I),
     'z1_owner_sum_workspace': ([_I64], _I64),
     'z1_owner_sum_waves': ([_I64], _I64),
-    'z1_owner_sum_bf16_waves': ([_P, _I, _I64, _F, _P, _P, _P, _I, _P], _I),
+    'z1_owner_sum_bf16_waves': ([_P, _I, _I64, _F, _P, _P, _P, _P], _I),
     'z1_reduce_waves': ([_P, _I64, _P, _P], _I),
     'z1_owner_sum_update': ([_P, _I, _I64, _F, _P, _P, _P, ctypes.POINTER(Z1UpdateScalars), _P], _I),
     'z1_owner_sum_update_noalloc': ([_P, _I, _I64, _F, _P, _P, ctypes.POINTER(Z1UpdateScalars), _P], _I),

@@ -26,13 +26,12 @@ _BY_OUT = weakref.WeakValueDictionary()      # address of a CEReduce's out -> it
 FUSE_NORM = True      # False: _sum leaves no partials and clip_grad_norm reads the gradients again (for comparisons)
 
 
-def sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=None, keep_end=True):
+def sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=None):
     """OUT[e] = bf16(sum_{k=0..WORLD-1} float(x_k[e]) * scale) for e in [BASE, END), in rank order, where x_R is OUT
     itself (rank R's own gradients) and the peers' contributions sit slot-major in S ([WORLD-1, G]: peer k < R in
     slot k, k > R in slot k-1).  In place in OUT, on the current stream.  waves (float64, nullable): the range's
-    norm partials per chunk (``ops.owner_sum_waves(END - BASE)`` of them); keep_end: leave the range's last 224 MB
-    in the MALL."""
-    ops.sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=waves, keep_end=keep_end)
+    norm partials per chunk (``ops.owner_sum_waves(END - BASE)`` of them)."""
+    ops.sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=waves)
 
 
 class PhaseNorm:
@@ -86,16 +85,13 @@ def _sum(self, ph):
     a, b = self.bounds[ph]
     if b <= a:
         return
-    # only the end of out is read first by the update (FusedAdamCast walks its gradients from the highest address
-    # down); a phase summed during the backward would only push it out of the MALL
-    keep = b == self.G
     if not FUSE_NORM:
-        sum_slots(self.staging, self.out, self.G, a, b, self.rank, 1.0 / self.world, self.world, keep_end=keep)
+        sum_slots(self.staging, self.out, self.G, a, b, self.rank, 1.0 / self.world, self.world)
         return
     pn = _phase_norm(self)
     o = pn.offset[ph]
     sum_slots(self.staging, self.out, self.G, a, b, self.rank, 1.0 / self.world, self.world,
-              waves=pn.waves[o:o + pn.count[ph]], keep_end=keep)
+              waves=pn.waves[o:o + pn.count[ph]])
     pn.summed[ph] = True
 
 

@@ -30,10 +30,10 @@
 //     Measured 0.25 ms for the 1.72 GB gradient (6.8 TB/s); the grid striding over all chunks (0.27 ms), one
 //     wave per chunk with hardware dispatch (0.40 ms), 4-chunk workgroups with hardware dispatch (0.34 ms),
 //     2-8 loads in flight per wave (0.28-0.31 ms) and fewer waves (0.35-0.59 ms) were all slower.
-//   * MALL reuse between passes: the pass before Adam (the norm, or the owner sum that writes the BF16 average)
-//     touches the last 256 (224) MB of the gradient with ordinary, allocating accesses, and Adam walks the
-//     chunks from the last one, so its first gradient reads hit the 256 MB MALL (measured 2.05 vs 2.10 ms for
-//     Adam on the C2 shard; 128-512 MB kept, or everything, measured the same or slower).
+//   * MALL reuse between passes: the norm pass reads the last 256 MB of the gradient with ordinary, allocating
+//     loads, and Adam walks the chunks from the last one, so its first gradient reads hit the 256 MB MALL
+//     (measured 2.05 vs 2.10 ms for Adam on the C2 shard; 128-512 MB kept, or everything, measured the same or
+//     slower).
 //   * No atomics anywhere; nothing but vector memory instructions write memory.  (The norm's final reduction is a
 //     second, one-workgroup launch: folding it into the last workgroup of the norm grid to finish, with an arrival
 //     counter, measured 75 us slower per step, because the grid's 2048 workgroups finish together.)
@@ -65,13 +65,12 @@ constexpr int kAdamWaves = 1;                                 // chunks (one per
 constexpr int kVec = 4;                                       // fp32 lanes of one 128-bit access
 constexpr int kGroups = 1;                                    // 128-bit groups per lane per array and chunk
 constexpr int64_t kChunk = (int64_t)kWave * kVec * kGroups;   // elements per chunk: one wave's share
-// The norm pass reads the last kMallKeepBytes of the gradient (the owner sum writes the last kOwnerSumKeepBytes of
-// the average) with ordinary, allocating accesses, so that they are still in the 256 MB MALL when the Adam pass --
-// which walks the chunks from the end -- reads them again.  Measured on C2 / C3: the norm keeps 256 MB (192-272 MB
-// no better); the owner sum 224 MB (C3 3.231-3.234 ms against 3.240-3.244 at 256 MB; 208-216 MB in between,
-// 232-240 MB slower), its allocating stores costing more than the norm's allocating loads.
+// The norm pass reads the last kMallKeepBytes of the gradient with ordinary, allocating loads, so that they are
+// still in the 256 MB MALL when the Adam pass -- which walks the chunks from the end -- reads them again (C2 Adam
+// 2.05 against 2.10 ms; 192-272 MB no better).  The owner sum keeps nothing: storing the average's last 224 MB with
+// allocating stores for Adam to read back gained nothing (C3 3.048 ms either way; the drop-in step 3.349 ms with
+// it, 3.334 ms without).
 constexpr int64_t kMallKeepBytes = 256ll << 20;
-constexpr int64_t kOwnerSumKeepBytes = 224ll << 20;
 constexpr int kAdamWgPerCu = 12;                              // resident Adam workgroups per CU (occupancy_lds)
 constexpr int kAdamGoutWgPerCu = 11;                          // the same, with FP32 gradient outputs (5 write streams)
 constexpr int kAdamFlatWgPerCu = 11;                          // the same, over contiguous flat buffers
@@ -120,11 +119,6 @@ __device__ __forceinline__ T ld_keep(const T* p) {       // ordinary load: alloc
 template <typename T>
 __device__ __forceinline__ void st(T* p, T x) {
     __builtin_nontemporal_store(x, (Z1_GLOBAL T*)p);
-}
-
-template <typename T>
-__device__ __forceinline__ void st_keep(T* p, T x) {     // ordinary store: allocates in L2 and the MALL
-    *(Z1_GLOBAL T*)p = x;
 }
 
 // Chunk of workgroup b: undoes the round-robin dispatch over the 8 XCDs (workgroup b runs on XCD b mod 8), so that
@@ -539,11 +533,11 @@ __device__ __host__ constexpr int64_t owner_sum_waves(int64_t n) {
     return n <= 0 ? 0 : (n + kSumShiftMax + kSumChunk - 1) / kSumChunk;
 }
 
-template <int W, bool KEEP>
+template <int W>
 __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, float scale, uint16_t* out,
                                                           float* out_sum, double* wave_partials, int vec,
-                                                          int64_t chunk_base, int64_t shift) {
-    const int64_t c = chunk_base + (int64_t)blockIdx.x;
+                                                          int64_t shift) {
+    const int64_t c = (int64_t)blockIdx.x;
     const int64_t e0 = c * kSumChunk + (int64_t)threadIdx.x * kSumVec - shift;
     double acc2 = 0.0;
     if (vec && e0 >= 0 && e0 + kSumVec <= n) {
@@ -564,8 +558,7 @@ __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, flo
         u2 o;
 #pragma unroll
         for (int w = 0; w < kSumVec / 2; ++w) o[w] = pack_bf16(a[2 * w] * scale, a[2 * w + 1] * scale);
-        if (KEEP) st_keep(reinterpret_cast<u2*>(out + e0), o);
-        else st(reinterpret_cast<u2*>(out + e0), o);
+        st(reinterpret_cast<u2*>(out + e0), o);
         if (out_sum) st(reinterpret_cast<f4*>(out_sum + e0), f4{a[0], a[1], a[2], a[3]});
         if (wave_partials) {
 #pragma unroll
@@ -590,7 +583,7 @@ __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, flo
     if (wave_partials) {
 #pragma unroll
         for (int off = kWave / 2; off > 0; off >>= 1) acc2 += __shfl_xor(acc2, off, kWave);
-        if (threadIdx.x == 0) wave_partials[chunk_base + chunk_of_block(blockIdx.x, gridDim.x)] = acc2;
+        if (threadIdx.x == 0) wave_partials[chunk_of_block(blockIdx.x, gridDim.x)] = acc2;
     }
 }
 
@@ -608,23 +601,15 @@ __global__ __launch_bounds__(kThreads) void reduce_partials_kernel(const double*
     if (threadIdx.x == 0) out[blockIdx.x] = t;
 }
 
-// Chunks [0, keep_from) with nontemporal stores of the average, then chunks [keep_from, nchunks) -- the end of the
-// average, which the Adam pass reads first -- with ordinary stores that leave it in the MALL.  Two launches: in one
-// kernel the compiler merges the two kinds of store into one ordinary store.
+// One launch over every chunk, with the kernel instantiated for the call's contribution count.
 template <int W>
-void launch_owner_sum(int world, int64_t nchunks, int64_t keep_from, size_t lds, hipStream_t st, const Srcs& s,
-                      int64_t n, float scale, uint16_t* out, float* out_sum, double* wave_partials, int vec,
-                      int64_t shift) {
+void launch_owner_sum(int world, int64_t nchunks, size_t lds, hipStream_t st, const Srcs& s, int64_t n, float scale,
+                      uint16_t* out, float* out_sum, double* wave_partials, int vec, int64_t shift) {
     if (world == W) {
-        if (keep_from > 0)
-            hipLaunchKernelGGL((owner_sum_kernel<W, false>), dim3((unsigned)keep_from), dim3(kWave), lds, st, s,
-                               n, scale, out, out_sum, wave_partials, vec, (int64_t)0, shift);
-        if (nchunks > keep_from)
-            hipLaunchKernelGGL((owner_sum_kernel<W, true>), dim3((unsigned)(nchunks - keep_from)), dim3(kWave),
-                               lds, st, s, n, scale, out, out_sum, wave_partials, vec, keep_from, shift);
+        hipLaunchKernelGGL((owner_sum_kernel<W>), dim3((unsigned)nchunks), dim3(kWave), lds, st, s, n, scale, out,
+                           out_sum, wave_partials, vec, shift);
     } else if constexpr (W > 1) {
-        launch_owner_sum<W - 1>(world, nchunks, keep_from, lds, st, s, n, scale, out, out_sum, wave_partials, vec,
-                                shift);
+        launch_owner_sum<W - 1>(world, nchunks, lds, st, s, n, scale, out, out_sum, wave_partials, vec, shift);
     }
 }
 
@@ -1344,8 +1329,7 @@ static int owner_sum_grid(const Srcs& s, int world, const uint16_t* out_avg, con
 // per-chunk partials' fixed-order reduction leaves the Z1_NORM_PARTIALS partials at its start (z1_owner_sum_bf16),
 // followed, with a tail, by the one-workgroup final reduction + scalar chain (z1_owner_sum_update).
 static int owner_sum(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
-                     float* out_sum, double* waves, double* workspace, const z1_update_scalars* tail, void* stream,
-                     bool keep_end = true) {
+                     float* out_sum, double* waves, double* workspace, const z1_update_scalars* tail, void* stream) {
     if (!contrib) return Z1_E_NULL;
     if (world < 1 || world > Z1_MAX_WORLD) return Z1_E_WORLD;
     if (n < 0) return Z1_E_SIZE;
@@ -1363,15 +1347,13 @@ static int owner_sum(const uint16_t* const* contrib, int world, int64_t n, float
     hipStream_t st = static_cast<hipStream_t>(stream);
     double* wave_partials = workspace ? workspace + Z1_NORM_PARTIALS : waves;
     if (nchunks > 0) {
-        const int64_t keep = keep_end ? kOwnerSumKeepBytes / (kSumChunk * (int64_t)sizeof(uint16_t)) : 0;
-        const int64_t keep_from = nchunks > keep ? nchunks - keep : 0;
         int dev = 0;
         size_t lds = 0;
         int rc = current_device(&dev);
         if (rc == Z1_OK) rc = occupancy_lds(dev, kOwnerSumWgPerCu, &lds);
         if (rc) return rc;
-        launch_owner_sum<Z1_MAX_WORLD>(world, nchunks, keep_from, lds, st, srcs, n, scale, out_avg, out_sum,
-                                       wave_partials, vec, shift);
+        launch_owner_sum<Z1_MAX_WORLD>(world, nchunks, lds, st, srcs, n, scale, out_avg, out_sum, wave_partials, vec,
+                                       shift);
         rc = launch_status();
         if (rc) return rc;
     }
@@ -1390,8 +1372,8 @@ int z1_owner_sum_bf16(const uint16_t* const* contrib, int world, int64_t n, floa
 }
 
 int z1_owner_sum_bf16_waves(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
-                            float* out_sum, double* waves, int keep_end, void* stream) {
-    return owner_sum(contrib, world, n, scale, out_avg, out_sum, waves, nullptr, nullptr, stream, keep_end != 0);
+                            float* out_sum, double* waves, void* stream) {
+    return owner_sum(contrib, world, n, scale, out_avg, out_sum, waves, nullptr, nullptr, stream);
 }
 
 int z1_reduce_waves(const double* waves, int64_t m, double* partials, void* stream) {

@@ -566,10 +566,9 @@ void owner_sum_update_(TensorList contribs, const Tensor& out, const Tensor& wor
 // The owner sum in the reference's staging layout (yoco/models/decoder/ce_reduce.py:59-74): the contribution of
 // peer k < rank in slot k of `staging`, of k > rank in slot k - 1, rank's own in `out`, summed in rank order into
 // out[base:end].  With `waves` (at least z1_owner_sum_waves(end - base) float64), the norm of the range's average
-// is left there per chunk (z1_owner_sum_bf16_waves), for reduce_waves_; keep_end as z1_owner_sum_bf16_waves takes
-// it.
+// is left there per chunk (z1_owner_sum_bf16_waves), for reduce_waves_.
 void sum_slots_(const Tensor& staging, const Tensor& out, int64_t G, int64_t base, int64_t end, int64_t rank,
-                double scale, int64_t world, const OptTensor& waves, bool keep_end) {
+                double scale, int64_t world, const OptTensor& waves) {
     TORCH_CHECK(staging.defined() && staging.is_cuda() && staging.scalar_type() == at::kBFloat16 &&
                 staging.is_contiguous(), "ce_reduce: staging must be a contiguous bf16 GPU tensor");
     TORCH_CHECK(out.defined() && out.is_cuda() && out.scalar_type() == at::kBFloat16 && out.is_contiguous(),
@@ -591,8 +590,7 @@ void sum_slots_(const Tensor& staging, const Tensor& out, int64_t G, int64_t bas
         ptrs[k] = k < rank ? s0 + k * G + base : (k == rank ? o0 + base : s0 + (k - 1) * G + base);
     OnDevice on(out);
     check_rc(api().owner_sum_bf16_waves(ptrs, static_cast<int>(world), end - base, static_cast<float>(scale),
-                                        o0 + base, nullptr, wp, keep_end ? 1 : 0, on.stream),
-             "z1_owner_sum_bf16_waves");
+                                        o0 + base, nullptr, wp, on.stream), "z1_owner_sum_bf16_waves");
 }
 
 // The fixed-order reduction of per-chunk norm partials (the first m of `waves`) into the norm's partials.
@@ -724,7 +722,7 @@ TORCH_LIBRARY(yoco_z1, m) {
           "Tensor(a8!)? flags, Tensor(a9!)? clip_log, Tensor? sample_size, float numer, float max_norm, "
           "float? factor_value) -> ()");
     m.def("sum_slots_(Tensor staging, Tensor(a1!) out, int G, int base, int end, int rank, float scale, "
-          "int world, Tensor(a8!)? waves=None, bool keep_end=True) -> ()");
+          "int world, Tensor(a8!)? waves=None) -> ()");
     m.def("reduce_waves_(Tensor waves, int m, Tensor(a2!) partials) -> ()");
     m.def("scale_up_(Tensor g16, Tensor(a1!) g32, Tensor factor) -> ()");
     m.def("cast_bf16_(Tensor p32, Tensor(a1!) p16) -> ()");

@@ -147,11 +147,10 @@ def owner_sum_update(contribs, out, scale, workspace, out_sum=None, sample_size=
                            flags_out, clip_log_out, sample_size, f32(numer), f32(max_norm), fv)
 
 
-def sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=None, keep_end=True):
+def sum_slots(S, OUT, G, BASE, END, R, scale, WORLD, waves=None):
     """The owner sum in the reference's staging layout, in place (yoco/models/decoder/ce_reduce.py:59-74).  waves
-    (float64, at least owner_sum_waves(END - BASE)): the range's norm partials per chunk, for reduce_waves.
-    keep_end: leave the range's last 224 MB in the MALL for the pass that reads them next."""
-    _OPS.sum_slots_(S, OUT, int(G), int(BASE), int(END), int(R), f32(scale), int(WORLD), waves, bool(keep_end))
+    (float64, at least owner_sum_waves(END - BASE)): the range's norm partials per chunk, for reduce_waves."""
+    _OPS.sum_slots_(S, OUT, int(G), int(BASE), int(END), int(R), f32(scale), int(WORLD), waves)
 
 
 def owner_sum_waves(n):

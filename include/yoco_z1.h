@@ -122,17 +122,14 @@ int64_t z1_owner_sum_workspace(int64_t n);
 int64_t z1_owner_sum_waves(int64_t n);
 
 /* z1_owner_sum_bf16 with the fused norm left per chunk: waves (z1_owner_sum_waves(n) doubles; nullable: no norm)
- * receives each chunk's FP64 sum of squares of the BF16 average (a fixed decomposition; nothing is reduced).  For a caller that sums a
- * gradient buffer one range at a time -- CEReduce._sum, once per backward phase
+ * receives each chunk's FP64 sum of squares of the BF16 average (a fixed decomposition; nothing is reduced).  For a
+ * caller that sums a gradient buffer one range at a time -- CEReduce._sum, once per backward phase
  * (yoco/models/decoder/ce_reduce.py:178-183,205-209,227) -- and wants the norm of the whole buffer without reading
  * it again, as yoco/tasks/zero1_fast.py:150 does: the ranges' partials, side by side in one array, go to
- * z1_reduce_waves once.  keep_end: the range's end is what the next pass reads first (the Adam launches walk their
- * gradients from the highest address down), so its last 224 MB are stored with allocating stores and stay in the
- * 256 MB MALL (z1_owner_sum_bf16 always does this); 0 for a range summed long before the update, all stores
- * streaming.  No counterpart in the reference, whose screen of a norm fused into the sum was not adopted
+ * z1_reduce_waves once.  No counterpart in the reference, whose screen of a norm fused into the sum was not adopted
  * (docs/training.md:335); the values are the same. */
 int z1_owner_sum_bf16_waves(const uint16_t* const* contrib, int world, int64_t n, float scale, uint16_t* out_avg,
-                            float* out_sum, double* waves, int keep_end, void* stream);
+                            float* out_sum, double* waves, void* stream);
 /* Fixed-order reduction of m per-chunk partials (z1_owner_sum_bf16_waves) into the Z1_NORM_PARTIALS partials that
  * z1_norm_clip and z1_update_scalars_run read. */
 int z1_reduce_waves(const double* waves, int64_t m, double* partials, void* stream);

@@ -72,10 +72,10 @@ def test_argument_errors_without_device_work(pkg):
     assert [L.z1_owner_sum_waves(n) for n in sizes] == [0, 1, 1, 2, 2, 2, 2, 3, 3]
     assert [L.z1_owner_sum_workspace(n) - 2048 for n in sizes] == [L.z1_owner_sum_waves(n) for n in sizes]
     assert L.z1_owner_sum_waves(-1) == -2
-    assert L.z1_owner_sum_bf16_waves(None, 1, 10, 1.0, ctypes.c_void_p(32), None, ctypes.c_void_p(64), 1,
+    assert L.z1_owner_sum_bf16_waves(None, 1, 10, 1.0, ctypes.c_void_p(32), None, ctypes.c_void_p(64),
                                      None) == -1                                   # no contributions
     assert L.z1_owner_sum_bf16_waves(ctypes.cast(arr, ctypes.c_void_p), 0, 10, 1.0, ctypes.c_void_p(32), None,
-                                     ctypes.c_void_p(64), 1, None) == -4
+                                     ctypes.c_void_p(64), None) == -4
     assert L.z1_reduce_waves(None, 4, ctypes.c_void_p(64), None) == -1
     assert L.z1_reduce_waves(ctypes.c_void_p(32), 4, None, None) == -1
     assert L.z1_reduce_waves(ctypes.c_void_p(32), -1, ctypes.c_void_p(64), None) == -2

@@ -380,22 +380,26 @@ def test_owner_sum_bit_exact(pkg, dev, world):
     assert abs(float(nr.item()) - ex) <= 1e-6 * ex
 
 
-KEEP_ELEMS = (224 << 20) // 2         # the owner sum's second launch: the average's last 224 MB (kept in the MALL)
-
-
-@pytest.mark.parametrize('n', [KEEP_ELEMS - 300, KEEP_ELEMS, KEEP_ELEMS + 1, KEEP_ELEMS + 257])
-def test_owner_sum_around_the_mall_keep_split(pkg, dev, n):
-    """Sizes where the owner sum's first launch covers no chunk (all of the average fits the kept window, the last
-    chunk whole or partial) or only one or two: the average, the fp32 sum and the fused norm against the oracle."""
+# sizes at the edges of the owner sum's chunk count (one partial per 256-element chunk of a grid shifted by up to 63
+# elements: 193 / 194, 449 / 450 elements need one more chunk), with the streams aligned or 134 bytes into a line
+@pytest.mark.parametrize('n', [1, 193, 194, 255, 256, 257, 449, 450, 65536 + 63])
+@pytest.mark.parametrize('offset', [0, 67])
+def test_owner_sum_at_chunk_count_edges(pkg, dev, n, offset):
+    """The average, the fp32 sum and the fused norm against the oracle, at sizes where the last chunk is whole,
+    partial or empty for the grid the streams' offset gives."""
     from faster_yoco_amd import ops
-    rng = np.random.default_rng(n)
+    rng = np.random.default_rng(n + offset)
     world = 2
     cs = [(rng.integers(0x3000, 0x4000, n, dtype=np.uint16) | (rng.integers(0, 2, n, dtype=np.uint16) << 15))
           .astype(np.uint16) for _ in range(world)]
     avg, s = oracle.owner_sum(cs, want_sum=True)
-    ts = [dev_bf16(c, dev) for c in cs]
-    out = torch.empty(n, dtype=torch.bfloat16, device=dev)
-    osum = torch.empty(n, dtype=torch.float32, device=dev)
+    ts = []
+    for c in cs:
+        buf = torch.zeros(n + 128, dtype=torch.bfloat16, device=dev)
+        buf[offset:offset + n].copy_(dev_bf16(c, dev))
+        ts.append(buf[offset:offset + n])
+    out = torch.zeros(n + 128, dtype=torch.bfloat16, device=dev)[offset:offset + n]
+    osum = torch.zeros(n + 128, dtype=torch.float32, device=dev)[offset:offset + n]
     part = ops.norm_workspace(dev, n)
     ops.owner_sum(ts, out, 1.0 / world, out_sum=osum, partials=part)
     nr = torch.zeros(1, device=dev)
