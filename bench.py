@@ -248,8 +248,9 @@ def dropin_step_timing(dev, hp, step0, steps=20, warmup=5, world=8, rank=3):
     12, BF16 copy 2, FP32 gradient 4 out); the norm reads nothing (the phase sums left its partials).  Timed
     steps chain: rank 3's own slot then holds the previous step's average, the same bytes and launches.  Also timed:
     the same with the norm read again from the gradients (ce_reduce.FUSE_NORM off, +2 B/param: its clip stage is
-    the BF16 norm pass over the 38 gradient views plus the clip chain), and the phase sums alone, on one stream, with
-    phase bounds on parameter boundaries and with bounds moved off every alignment."""
+    the BF16 norm pass over the 38 gradient views plus the clip chain), that norm pass alone (back to back), and the
+    phase sums alone, on one stream, with phase bounds on parameter boundaries and with bounds moved off every
+    alignment."""
     import torch
     from faster_yoco_amd import ce_reduce, configs, layout, standins, zero1_fast
     shapes = configs.shapes('c3')
@@ -375,6 +376,22 @@ def dropin_step_timing(dev, hp, step0, steps=20, warmup=5, world=8, rank=3):
         res['norm_read_again_ms'] = round(ms_u, 4)
         res['norm_read_again_stage_ms'] = {k: round(v, 4) for k, v in stages().items()}
         ce_reduce.FUSE_NORM = True
+        # that norm pass alone: the BF16 norm over the 38 gradient views (a norm-only table, rows in address order
+        # as the clip builds it), 20 launches back to back between two events; in the step it follows the phase
+        # sums, whose stores are still draining (its clip stage above)
+        from faster_yoco_amd import kernels, ops
+        tab = kernels.Table([(v.view(-1), None, None, None, None, v.numel())
+                             for v in sorted(views, key=lambda t: t.data_ptr())], dev)
+        parts = ops.norm_workspace(dev)
+
+        def norms():
+            for _ in range(20):
+                ops.grad_sumsq(tab, parts)
+        norms()
+        us = sorted(timed(norms, 1)[0] * 1e3 / 20 for _ in range(5))[2]
+        res['norm_bf16_pass'] = {'kernel': 'sumsq_kernel<1, 128>', 'bytes': 2 * G, 'us_back_to_back': round(us, 1),
+                                 'GBps': round(2 * G / (us * 1e-6) / 1e9, 1)}
+        del tab
 
         def phases_one_stream():                                # the kernels alone: no cross-stream waits
             for ph in range(len(ce.bounds)):

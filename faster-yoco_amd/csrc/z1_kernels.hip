@@ -285,8 +285,9 @@ __global__ __launch_bounds__(kWave) void adam_flat_kernel(Row w, int64_t nchunks
 }
 
 // -------------------------------------------------------------------------------------- deterministic norm
-// Sum over the workgroup, result valid in thread 0: xor butterfly inside each wave64 (a + b == b + a exactly, so
-// every lane ends with the same bits), then the four wave sums in wave order.
+// Sum over a workgroup of NT threads, result valid in thread 0: xor butterfly inside each wave64 (a + b == b + a
+// exactly, so every lane ends with the same bits), then the wave sums in wave order.
+template <int NT = kThreads>
 __device__ __forceinline__ double block_sum(double x, double* lds) {
 #pragma unroll
     for (int off = kWave / 2; off > 0; off >>= 1) x += __shfl_xor(x, off, kWave);
@@ -295,7 +296,7 @@ __device__ __forceinline__ double block_sum(double x, double* lds) {
     double s = 0.0;
     if (threadIdx.x == 0) {
 #pragma unroll
-        for (int w = 0; w < kThreads / kWave; ++w) s += lds[w];
+        for (int w = 0; w < NT / kWave; ++w) s += lds[w];
     }
     return s;
 }
@@ -411,12 +412,17 @@ __device__ __forceinline__ void sumsq_chunk(const Row& r, int64_t c, int lane, d
 // C2's size, 4.6 TB/s, even with two chunks' loads in flight); runs of 2, 4, 8 and 16 chunks measured 143, 135,
 // 136 and 143 us.  Either way the order is fixed, so the partials are deterministic.
 constexpr int kSumsqBf16Span = 4;
+constexpr int kSumsqBf16Threads = 128;                       // 2 waves per norm workgroup for BF16
+// r is row t, held in registers until a chunk at or past next0 (row t + 1's first chunk) needs the next row.
 template <int GDT, bool KEEP>
-__device__ __forceinline__ void sumsq_range(const Row* __restrict__ rows, int nrows, int& t, int64_t& c, int64_t end,
-                                            int64_t step, int lane, double& acc) {
+__device__ __forceinline__ void sumsq_range(const Row* __restrict__ rows, int nrows, int& t, Row& r, int64_t& next0,
+                                            int64_t& c, int64_t end, int64_t step, int lane, double& acc) {
     for (; c < end; c += step) {
-        t = advance_row(rows, nrows, t, c);
-        const Row r = rows[t];
+        if (c >= next0) {
+            t = advance_row(rows, nrows, t, c);
+            r = rows[t];
+            next0 = t + 1 < nrows ? rows[t + 1].chunk0 : INT64_MAX;
+        }
         if (GDT == Z1_BF16) {
             constexpr int S = kSumsqBf16Span, L = kSumsqBf16Span / 2;
             const uint16_t* g = static_cast<const uint16_t*>(r.g) + (c - r.chunk0) * kChunk;
@@ -448,18 +454,25 @@ __device__ __forceinline__ void sumsq_range(const Row* __restrict__ rows, int nr
     }
 }
 
-// Fixed grid of Z1_NORM_PARTIALS workgroups (a multiple of 8): the 256 workgroups b with b & 7 == x cover eighth x
-// of the chunks, wave w of them taking chunks lo_x + w, lo_x + w + 1024, ... (a workgroup covers 4 consecutive
-// chunks = 1024 contiguous elements per step; for BF16, runs of kSumsqBf16Span chunks starting at lo_x + 4w,
-// lo_x + 4w + 4096, ...: 4 consecutive runs = 4096 elements per step); each lane adds its exact squares in that
-// fixed order.
+// Fixed grid of Z1_NORM_PARTIALS workgroups (a multiple of 8) of NT threads: the 256 workgroups b with b & 7 == x
+// cover eighth x of the chunks, wave w of workgroup j taking the runs of `span` chunks that start at
+// lo_x + span (j W + w), then every span x 256 W chunks on (W = NT / 64 waves per workgroup; FP32: span 1, W 4,
+// 1024 contiguous elements per workgroup step; BF16: span kSumsqBf16Span, W 2, 2048).  Each lane adds its exact
+// squares in that fixed order.  Either way one step of an XCD's workgroups spans 1 MB of its eighth (4 waves per
+// workgroup for BF16, a 2 MB window, measured 1-3 % slower: 125.1 against 124.4 us back to back over C2's 38
+// tensors, 136 against 133.5 us right after the owner sum that wrote them).
 // Chunks [keep_from, nchunks) are read with ordinary loads (two loops, so that the two kinds of load stay apart):
 // they are where the Adam pass starts (adam_cast_kernel walks the chunks from the last one down), so its first
 // gradient reads hit the MALL.
-template <int GDT>
-__global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__ rows, int nrows, int64_t nchunks,
-                                                         int64_t keep_from, double* __restrict__ partials) {
-    __shared__ double lds[kThreads / kWave];
+// Each wave's first row comes from the rows' first chunks staged in LDS (tables of up to kSumsqLdsRows rows): one
+// load instead of a binary search of dependent scalar loads at the start of every wave.
+constexpr int kSumsqLdsRows = 512;
+template <int GDT, int NT>
+__global__ __launch_bounds__(NT) void sumsq_kernel(const Row* __restrict__ rows, int nrows, int64_t nchunks,
+                                                   int64_t keep_from, double* __restrict__ partials) {
+    constexpr int W = NT / kWave;
+    __shared__ double lds[W];
+    __shared__ int64_t first[kSumsqLdsRows];
     const int lane = threadIdx.x & (kWave - 1);
     // workgroup b strides through eighth (b & 7) of the chunks only: the eighth the XCD it is dispatched to
     // (b mod 8) owns, as in chunk_of_block (0.257 vs 0.268 ms on C2, 2.11 vs 2.34 ms on C4 for the whole grid
@@ -467,17 +480,30 @@ __global__ __launch_bounds__(kThreads) void sumsq_kernel(const Row* __restrict__
     const int64_t x = blockIdx.x & 7, j = blockIdx.x >> 3;
     const int64_t Q = nchunks >> 3, R = nchunks & 7;
     const int64_t lo = x * Q + (x < R ? x : R), hi = lo + Q + (x < R ? 1 : 0);
-    const int64_t nw = (int64_t)(gridDim.x >> 3) * (kThreads / kWave);
+    const int64_t nw = (int64_t)(gridDim.x >> 3) * W;
     const int64_t span = GDT == Z1_BF16 ? kSumsqBf16Span : 1;   // chunks a wave takes per step
-    const int64_t w0 = lo + span * (j * (kThreads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
+    const int64_t w0 = lo + span * (j * W + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave));
     int64_t split = keep_from > lo ? (keep_from < hi ? keep_from : hi) : lo;
     split = lo + (split - lo + span - 1) / span * span;   // on the run grid: no run straddles the two loops
-    double acc = 0.0;
     int t = 0;
+    if (nrows > 1 && nrows <= kSumsqLdsRows) {            // uniform over the workgroup (kernel arguments)
+        for (int i = threadIdx.x; i < nrows; i += NT) first[i] = rows[i].chunk0;
+        __syncthreads();
+        int a = 0, z = nrows - 1;                         // the last row whose first chunk is <= w0
+        while (a < z) {
+            const int mid = (a + z + 1) >> 1;
+            if (first[mid] <= w0) a = mid;
+            else z = mid - 1;
+        }
+        t = __builtin_amdgcn_readfirstlane(a);
+    }
+    Row r = {};
+    int64_t next0 = 0;                                    // the first chunk loads row t (advance_row from t)
+    double acc = 0.0;
     int64_t c = w0;
-    sumsq_range<GDT, false>(rows, nrows, t, c, split < hi ? split : hi, span * nw, lane, acc);
-    sumsq_range<GDT, true>(rows, nrows, t, c, hi, span * nw, lane, acc);
-    const double s = block_sum(acc, lds);
+    sumsq_range<GDT, false>(rows, nrows, t, r, next0, c, split < hi ? split : hi, span * nw, lane, acc);
+    sumsq_range<GDT, true>(rows, nrows, t, r, next0, c, hi, span * nw, lane, acc);
+    const double s = block_sum<NT>(acc, lds);
     if (threadIdx.x == 0) partials[blockIdx.x] = s;
 }
 
@@ -1135,11 +1161,11 @@ static int launch_sumsq(const z1_table* table, double* partials, const z1_update
     hipStream_t s = static_cast<hipStream_t>(stream);
     const int64_t kf = keep_from(table);
     if (table->g_dtype == Z1_F32)
-        hipLaunchKernelGGL(sumsq_kernel<Z1_F32>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows_dev, table->nchunks, kf, partials);
+        hipLaunchKernelGGL((sumsq_kernel<Z1_F32, kThreads>), dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s,
+                           table->rows, table->nrows_dev, table->nchunks, kf, partials);
     else
-        hipLaunchKernelGGL(sumsq_kernel<Z1_BF16>, dim3(Z1_NORM_PARTIALS), dim3(kThreads), 0, s, table->rows,
-                           table->nrows_dev, table->nchunks, kf, partials);
+        hipLaunchKernelGGL((sumsq_kernel<Z1_BF16, kSumsqBf16Threads>), dim3(Z1_NORM_PARTIALS),
+                           dim3(kSumsqBf16Threads), 0, s, table->rows, table->nrows_dev, table->nchunks, kf, partials);
     rc = launch_status();
     if (rc || !tail) return rc;
     hipLaunchKernelGGL(scalars_kernel, dim3(1), dim3(kThreads), 0, s, partials, *tail);
