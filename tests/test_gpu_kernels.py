@@ -318,6 +318,43 @@ def test_norm_heavy_tails_deterministic_and_scaling(pkg, dev):
     assert abs(gpu_norm(pkg, dev, perm)[0] - ex) <= 1e-6 * ex
 
 
+@pytest.mark.parametrize('nrows', [300, 511, 512, 513, 1000])
+@pytest.mark.parametrize('g_bf16', [False, True])
+def test_norm_over_many_rows(pkg, dev, nrows, g_bf16):
+    """Tables of nrows device rows around the norm kernel's LDS staging of the rows' first chunks (up to 512; more
+    fall back to the search from row 0), plus zero-size rows (absent from the device table), sizes off the
+    256-element chunk, and the same rows as views of one buffer at odd offsets (BF16: not 8-byte aligned, the
+    element-wise path): within 1 ulp of the exact norm, bit-identical on a second run."""
+    from faster_yoco_amd import ops
+    rng = np.random.default_rng(nrows + 7 * g_bf16)
+    sizes = rng.integers(1, 1200, nrows)                 # nrows device rows
+    sizes[rng.choice(nrows, nrows // 10, replace=False)] = 256 * rng.integers(1, 5, nrows // 10)
+    sizes = np.insert(sizes, rng.integers(0, nrows + 1, nrows // 10), 0)   # and zero-size rows between them
+    grads = []
+    for i, n in enumerate(sizes):
+        g = (rng.standard_normal(int(n)) * 10.0 ** rng.integers(-6, 1)).astype(np.float32)
+        grads.append(oracle.bf16_rne(g) if g_bf16 else g)
+    ex = exact_norm([g for g in grads if g.size])
+    a = gpu_norm(pkg, dev, grads)
+    assert gpu_norm(pkg, dev, grads) == a
+    assert oracle.ulp_diff_f32(a[0], np.float32(ex)) <= 1
+    # the same gradients as views of one buffer, each starting one element past the last
+    flat = np.concatenate([np.zeros(1, grads[0].dtype)] + [np.concatenate([g, np.zeros(1, g.dtype)]) for g in grads])
+    buf = dev_bf16(flat, dev) if g_bf16 else dev_f32(flat, dev)
+    rows, o = [], 1
+    for g in grads:
+        rows.append((buf[o:o + g.size], None, None, None, None, g.size))
+        o += g.size + 1
+    table = ops.Table(rows, dev)
+    part = ops.norm_workspace(dev)
+    ops.grad_sumsq(table, part)
+    nr = torch.zeros(1, device=dev)
+    ops.norm_clip(part, norm_out=nr, max_norm=1.0)
+    torch.cuda.synchronize()
+    assert oracle.ulp_diff_f32(np.float32(nr.item()), np.float32(ex)) <= 1
+    table.close()
+
+
 def test_norm_edge_cases(pkg, dev):
     z = [np.zeros(1000, np.float32)]
     nr, gn, fo = gpu_norm(pkg, dev, z)
