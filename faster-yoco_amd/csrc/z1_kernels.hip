@@ -60,7 +60,7 @@ namespace {
 
 // Launch geometry (the measured choices on MI355X; alternatives and their timings are recorded with the design):
 constexpr int kWave = 64;
-constexpr int kThreads = 256;                                 // norm and one-workgroup reduction workgroups
+constexpr int kThreads = 256;                                 // FP32 norm and one-workgroup reduction workgroups
 constexpr int kAdamWaves = 1;                                 // chunks (one per wave) per Adam workgroup
 constexpr int kVec = 4;                                       // fp32 lanes of one 128-bit access
 constexpr int kGroups = 1;                                    // 128-bit groups per lane per array and chunk
