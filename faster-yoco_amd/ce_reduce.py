@@ -92,6 +92,10 @@ def _sum(self, ph):
     o = pn.offset[ph]
     sum_slots(self.staging, self.out, self.G, a, b, self.rank, 1.0 / self.world, self.world,
               waves=pn.waves[o:o + pn.count[ph]])
+    # the phases run on CEReduce's sum stream and on the current one, and clip_grad_norm reads the partials on its
+    # stream: each use is recorded, so that a PhaseNorm dropped when the bounds change frees its partials only
+    # after every stream is past them
+    pn.waves.record_stream(torch.cuda.current_stream(self.out.device))
     pn.summed[ph] = True
 
 
@@ -113,6 +117,7 @@ def take_norm_partials(grads):
     if pos != pn.out_ptr + 2 * pn.G:
         return None
     pn.summed = [False] * len(pn.bounds)
+    pn.waves.record_stream(torch.cuda.current_stream(pn.device))       # read by the caller on this stream
     return pn.waves, pn.m
 
 

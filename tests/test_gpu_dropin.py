@@ -400,23 +400,31 @@ def test_ce_reduce_phase_norm_feeds_clip_grad_norm(pkg, dev, monkeypatch):
                 used['pass'] += 1
                 return _real(*a, **k)
             monkeypatch.setattr(ops, name, counted)
-        for step, (max_norm, fused) in enumerate(((1.0, True), (0.01, True), (1.0, False), (1.0, 'stale')), 1):
+        two = [[0, ends[3]], [ends[3], G]]              # other phase bounds: the CEReduce's PhaseNorm is made again
+        steps = ((1.0, True, bounds), (0.01, True, bounds), (1.0, False, bounds), (1.0, 'stale', bounds),
+                 (1.0, True, two))
+        for step, (max_norm, fused, bnds) in enumerate(steps, 1):
             S = oracle.bf16_rne((rng.standard_normal((W - 1) * G) * 1e-2).astype(np.float32))
             OUT = oracle.bf16_rne((rng.standard_normal(G) * 1e-2).astype(np.float32))
-            ce = cls(torch.from_numpy(S.view(np.int16)).to(dev).view(torch.bfloat16),
-                     torch.from_numpy(OUT.view(np.int16)).to(dev).view(torch.bfloat16), G, bounds, R, W)
+            if step < 5:
+                ce = cls(torch.from_numpy(S.view(np.int16)).to(dev).view(torch.bfloat16),
+                         torch.from_numpy(OUT.view(np.int16)).to(dev).view(torch.bfloat16), G, bnds, R, W)
+            else:                                  # the same CEReduce and out, new contents and bounds
+                ce.staging.copy_(torch.from_numpy(S.view(np.int16)).to(dev).view(torch.bfloat16))
+                ce.out.copy_(torch.from_numpy(OUT.view(np.int16)).to(dev).view(torch.bfloat16))
+                ce.bounds = bnds
             avg = OUT.copy()
-            for a, b in bounds:
+            for a, b in bnds:
                 oracle.sum_slots(S, avg, G, a, b, R, 1.0 / W, W)
             cur = torch.cuda.current_stream(dev)
             side.wait_stream(cur)
             with torch.cuda.stream(side):
-                for ph in range(len(bounds) - 1):
+                for ph in range(len(bnds) - 1):
                     ce._sum(ph)
             if fused != 'stale':
-                ce._sum(len(bounds) - 1)
+                ce._sum(len(bnds) - 1)
             else:                                  # the last phase summed without its partials: no fused norm
-                ce_reduce.sum_slots(ce.staging, ce.out, G, *bounds[-1], R, 1.0 / W, W)
+                ce_reduce.sum_slots(ce.staging, ce.out, G, *bnds[-1], R, 1.0 / W, W)
             cur.wait_stream(side)
             off = 0
             for p, n in zip(params, numels):
