@@ -9,8 +9,8 @@ arguments, and collects in ``.cast`` the addresses of the masters whose BF16 cop
   * what a parameter list needs -- its tables, the BF16 destinations found in ``dest``, the masters they belong to
     -- is worked out once per list of masters and set of folded rows (keyed by the masters' addresses and sizes,
     as ``dest`` is keyed by address) and reused while they recur; each call's tensors are still checked, by the
-    operator; a table's rows are ordered by their gradients' addresses (the launch starts at the highest, which is
-    what the pass before it wrote last);
+    operator; a table's rows are ordered by their gradients' addresses (the launch starts at the highest, where a
+    norm pass over the same gradients, whose table is ordered alike, ends with allocating loads);
   * ``fold`` / ``fold_factor`` (set by zero1_fast.step with the fused Adam) name masters whose BF16 gradient the
     kernel reads times the factor, in place of the FP32 gradient a scale pass would have written first: the same
     products g' = fp32(float(g16) * factor).  With ``fold_writes`` (zero1_fast's default) the kernel also stores
@@ -101,9 +101,9 @@ class FusedAdamCast:
         for f in (False, True):
             if rows[f]:
                 # rows in the order of their gradients' addresses: the launch walks from the last row down, so it
-                # starts at the highest gradient address -- the end of a flat gradient buffer, which the owner sum
-                # that wrote it last left in the MALL (CEReduce's last phase, ce_reduce.py:227) -- whatever order
-                # the parameters come in (CEReduce lays them out by backward phase, :122-140)
+                # starts at the highest gradient address -- where the norm pass over the same gradients (its table
+                # ordered alike) read its last 256 MB with allocating loads, still in the MALL -- whatever order
+                # the parameters come in (CEReduce lays them out by backward phase, ce_reduce.py:122-140)
                 order = sorted(range(len(rows[f])), key=lambda j: rows[f][j][0].data_ptr())
                 srows = [rows[f][j] for j in order]
                 sidx = [idx[f][j] for j in order]

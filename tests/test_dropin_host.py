@@ -90,7 +90,7 @@ def test_take_norm_partials_needs_gradients_that_are_the_views_of_out(pkg):
 
 def test_fused_adam_cast_orders_a_tables_rows_by_gradient_address(pkg):
     """FusedAdamCast builds each table with its rows sorted by the gradients' addresses (the launch then starts at
-    the highest one, what the pass before it wrote last) and maps the call's lists to that order."""
+    the highest one, where a norm pass over the same gradients ends) and maps the call's lists to that order."""
     from faster_yoco_amd import fused_adam_cast
     made = []
 
