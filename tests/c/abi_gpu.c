@@ -8,7 +8,9 @@
  *      gradients bound with z1_table_set_grads (one of them misaligned), runs as two launches over row ranges
  *      bounded by z1_table_info's row count (empty row included), again bit-exact;
  *   2. the owner sum of 8 BF16 contributions with the fused norm: average and FP32 sum bit-exact, norm within
- *      1e-6 of the average's exact norm; z1_owner_sum_update (with the clip chain, twice, then on a shorter
+ *      1e-6 of the average's exact norm; the same sum one range at a time with z1_owner_sum_bf16_waves (odd
+ *      bounds, an empty range) and the partials reduced once by z1_reduce_waves: the same average and sum bits,
+ *      the norm within 1 ulp of the exact one; z1_owner_sum_update (with the clip chain, twice, then on a shorter
  *      input with the same workspace) gives the same bits as z1_owner_sum_bf16 + z1_norm_clip;
  *   3. the embedding gradient (workspace query, ids with repeats, out-of-range ids and padding, x 1/8 after) at
  *      5000 rows (aten's sort-path order) and 1000 rows (its order for few indices): bit-exact;
@@ -254,6 +256,43 @@ static int owner_sum(void) {
     EXPECT(same_f32(hsum, esum, n));
     const double exact = sqrt(oracle_sumsq_bf16(eavg, n));
     EXPECT(fabs((double)nrm - exact) <= 1e-6 * exact);
+    /* the same sum one range at a time (CEReduce's phases: odd bounds, an empty range), each range's per-chunk norm
+     * partials side by side in one array and reduced once: average and FP32 sum bit-exact, the norm within 1 fp32
+     * ulp of the correctly rounded exact one */
+    {
+        const int64_t cut[5] = {0, 30001, 30001, 77777, n};
+        int64_t m = 0;
+        for (int r = 0; r < 4; ++r) {
+            const int64_t w = z1_owner_sum_waves(cut[r + 1] - cut[r]);
+            EXPECT(w >= 0);
+            m += w;
+        }
+        double* dwv;
+        HIP_OK(hipMalloc((void**)&dwv, (size_t)(m > 0 ? m : 1) * 8));
+        HIP_OK(hipMemset(davg, 0, n * 2));
+        HIP_OK(hipMemset(dsum, 0, n * 4));
+        int64_t off = 0;
+        for (int r = 0; r < 4; ++r) {
+            const int64_t a = cut[r], len = cut[r + 1] - cut[r];
+            const uint16_t* src[W];
+            for (int k = 0; k < W; ++k) src[k] = dc[k] + a;
+            Z1_OK_(z1_owner_sum_bf16_waves(src, W, len, 0.125f, davg + a, dsum + a, dwv + off, NULL));
+            off += z1_owner_sum_waves(len);
+        }
+        EXPECT(off == m);
+        Z1_OK_(z1_reduce_waves(dwv, m, dws, NULL));
+        Z1_OK_(z1_norm_clip(dws, NULL, 1.0f, dnr, NULL, NULL, 0.0f, NULL));
+        HIP_OK(hipDeviceSynchronize());
+        float nrm2;
+        HIP_OK(hipMemcpy(havg, davg, n * 2, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(hsum, dsum, n * 4, hipMemcpyDeviceToHost));
+        HIP_OK(hipMemcpy(&nrm2, dnr, 4, hipMemcpyDeviceToHost));
+        EXPECT(memcmp(havg, eavg, (size_t)n * 2) == 0);
+        EXPECT(same_f32(hsum, esum, n));
+        const int64_t du = (int64_t)bits(nrm2) - (int64_t)bits((float)exact);
+        EXPECT(du >= -1 && du <= 1);
+        HIP_OK(hipFree(dwv));
+    }
     /* z1_owner_sum_update against z1_owner_sum_bf16 + z1_norm_clip: twice on n, then on a shorter input with the
      * same workspace */
     float* dsc;
