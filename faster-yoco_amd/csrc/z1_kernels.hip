@@ -121,6 +121,24 @@ __device__ __forceinline__ void st(T* p, T x) {
     __builtin_nontemporal_store(x, (Z1_GLOBAL T*)p);
 }
 
+// The update's streaming stores (Adam's p, m, v, BF16 copy and FP32 gradient outputs; the owner sum's average) go
+// out as buffer stores whose cache-policy bits mark them system scope as well as nontemporal (sc0 sc1 nt; gfx950's
+// store bits: sc0 = 1, nt = 2, sc1 = 16), which the L2 writes through at once rather than keeping dirty lines for a
+// later write-back.  Measured against the nontemporal global stores above, interleaved on one box: C2 update
+// 2.179 against 2.197-2.228 ms, C3 2.995-3.002 against 3.051-3.053 ms, the drop-in step 3.268-3.282 against
+// 3.325-3.329 ms (the same stores with nt alone, through a buffer, measured like the global ones; the loads marked
+// the same way were slower: C3 3.27 ms).  The descriptor covers one wave's chunk (word 3 = 0x00020000: the raw
+// 32-bit data format of gfx9 buffer resources), so the offset is the lane's byte offset within it.
+constexpr int kStreamStorePolicy = 1 | 2 | 16;
+__device__ __forceinline__ void st_stream(float* base, int bytes, int off, f4 x) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, x), r, off, 0, kStreamStorePolicy);
+}
+__device__ __forceinline__ void st_stream(uint16_t* base, int bytes, int off, u2 x) {
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000);
+    __builtin_amdgcn_raw_buffer_store_b64(x, r, off, 0, kStreamStorePolicy);
+}
+
 // Chunk of workgroup b: undoes the round-robin dispatch over the 8 XCDs (workgroup b runs on XCD b mod 8), so that
 // each XCD streams one contiguous eighth of the chunks.  Used by the scale and cast passes; Adam and the owner sum
 // measured faster with the plain b -> b map (consecutive chunks interleaved over the XCDs: C2 update 2.283 vs
@@ -218,15 +236,16 @@ __device__ __forceinline__ void adam_chunk(const Row& r, float* go, int64_t base
         }
 #pragma unroll
         for (int u = 0; u < kGroups; ++u) {
-            const int64_t i = base + (int64_t)(u * kWave + lane) * kVec;
-            st(reinterpret_cast<f4*>(r.p + i), p[u]);
-            st(reinterpret_cast<f4*>(r.m + i), m[u]);
-            st(reinterpret_cast<f4*>(r.v + i), v[u]);
+            // lane offsets within the chunk [base, base + kChunk) of each stream
+            const int o4 = (u * kWave + lane) * kVec * 4, o2 = (u * kWave + lane) * kVec * 2;
+            st_stream(r.p + base, (int)kChunk * 4, o4, p[u]);
+            st_stream(r.m + base, (int)kChunk * 4, o4, m[u]);
+            st_stream(r.v + base, (int)kChunk * 4, o4, v[u]);
             if (r.p16) {
                 const u2 h = u2{pack_bf16(p[u][0], p[u][1]), pack_bf16(p[u][2], p[u][3])};
-                st(reinterpret_cast<u2*>(r.p16 + i), h);
+                st_stream(r.p16 + base, (int)kChunk * 2, o2, h);
             }
-            if (GOUT && go) st(reinterpret_cast<f4*>(go + i), g[u]);
+            if (GOUT && go) st_stream(go + base, (int)kChunk * 4, o4, g[u]);
         }
     } else {
         const int64_t cnt = rem < kChunk ? rem : kChunk;
@@ -584,8 +603,11 @@ __global__ __launch_bounds__(kWave) void owner_sum_kernel(Srcs s, int64_t n, flo
         u2 o;
 #pragma unroll
         for (int w = 0; w < kSumVec / 2; ++w) o[w] = pack_bf16(a[2 * w] * scale, a[2 * w + 1] * scale);
-        st(reinterpret_cast<u2*>(out + e0), o);
-        if (out_sum) st(reinterpret_cast<f4*>(out_sum + e0), f4{a[0], a[1], a[2], a[3]});
+        // the chunk's first element (the range's, for a first chunk the shift moves before it): every lane of this
+        // path writes [e0, e0 + 4) within [cb, cb + kSumChunk)
+        const int64_t cb = c * kSumChunk - shift > 0 ? c * kSumChunk - shift : 0;
+        st_stream(out + cb, (int)kSumChunk * 2, (int)(e0 - cb) * 2, o);
+        if (out_sum) st_stream(out_sum + cb, (int)kSumChunk * 4, (int)(e0 - cb) * 4, f4{a[0], a[1], a[2], a[3]});
         if (wave_partials) {
 #pragma unroll
             for (int w = 0; w < kSumVec / 2; ++w) {
