@@ -121,14 +121,16 @@ __device__ __forceinline__ void st(T* p, T x) {
     __builtin_nontemporal_store(x, (Z1_GLOBAL T*)p);
 }
 
-// The update's streaming stores (Adam's p, m, v, BF16 copy and FP32 gradient outputs; the owner sum's average) go
-// out as buffer stores whose cache-policy bits mark them system scope as well as nontemporal (sc0 sc1 nt; gfx950's
-// store bits: sc0 = 1, nt = 2, sc1 = 16), which the L2 writes through at once rather than keeping dirty lines for a
-// later write-back.  Measured against the nontemporal global stores above, interleaved on one box: C2 update
-// 2.179 against 2.197-2.228 ms, C3 2.995-3.002 against 3.051-3.053 ms, the drop-in step 3.268-3.282 against
-// 3.325-3.329 ms (the same stores with nt alone, through a buffer, measured like the global ones; the loads marked
-// the same way were slower: C3 3.27 ms).  The descriptor covers one wave's chunk (word 3 = 0x00020000: the raw
-// 32-bit data format of gfx9 buffer resources), so the offset is the lane's byte offset within it.
+// The update's streaming stores (Adam's p, m, v, BF16 copy and FP32 gradient outputs; the owner sum's average; the
+// scale and cast passes) go out as buffer stores whose cache-policy bits mark them system scope as well as
+// nontemporal (sc0 sc1 nt; gfx950's store bits: sc0 = 1, nt = 2, sc1 = 16), which the L2 writes through at once
+// rather than keeping dirty lines for a later write-back.  Measured against the nontemporal global stores above,
+// interleaved on one box: C2 update 2.179 against 2.197-2.228 ms, C3 2.995-3.002 against 3.051-3.053 ms, the drop-in
+// step 3.268-3.282 against 3.325-3.329 ms, the scale pass over 430M elements 0.403 against 0.410 ms.  The same stores
+// with nt alone, through a buffer, measured like the global ones; the loads marked the same way were slower (C3
+// 3.27 ms), and so were the embedding gradient's row stores, which keep nt.  The descriptor covers one wave's chunk
+// (word 3 = 0x00020000: the raw 32-bit data format of gfx9 buffer resources), so the offset is the lane's byte offset
+// within it.
 constexpr int kStreamStorePolicy = 1 | 2 | 16;
 __device__ __forceinline__ void st_stream(float* base, int bytes, int off, f4 x) {
     const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, 0x00020000);
@@ -736,8 +738,8 @@ __global__ __launch_bounds__(kWave) void scale_up_kernel(const uint16_t* __restr
         for (int u = 0; u < 2; ++u) h[u] = ld(reinterpret_cast<const u2*>(g16 + e0 + u * (kPassChunk / 2)) + lane);
 #pragma unroll
         for (int u = 0; u < 2; ++u)
-            st(reinterpret_cast<f4*>(g32 + e0 + u * (kPassChunk / 2)) + lane,
-               f4{bf16_lo(h[u].x) * f, bf16_hi(h[u].x) * f, bf16_lo(h[u].y) * f, bf16_hi(h[u].y) * f});
+            st_stream(g32 + e0, (int)kPassChunk * 4, (int)((u * (kPassChunk / 2) + lane * 4) * 4),
+                      f4{bf16_lo(h[u].x) * f, bf16_hi(h[u].x) * f, bf16_lo(h[u].y) * f, bf16_hi(h[u].y) * f});
         return;
     }
     const int64_t e1 = e0 + kPassChunk < n ? e0 + kPassChunk : n;
@@ -754,8 +756,8 @@ __global__ __launch_bounds__(kWave) void cast_bf16_kernel(const float* __restric
         for (int u = 0; u < 2; ++u) a[u] = ld(reinterpret_cast<const f4*>(p32 + e0 + u * (kPassChunk / 2)) + lane);
 #pragma unroll
         for (int u = 0; u < 2; ++u)
-            st(reinterpret_cast<u2*>(p16 + e0 + u * (kPassChunk / 2)) + lane,
-               u2{pack_bf16(a[u].x, a[u].y), pack_bf16(a[u].z, a[u].w)});
+            st_stream(p16 + e0, (int)kPassChunk * 2, (int)((u * (kPassChunk / 2) + lane * 4) * 2),
+                      u2{pack_bf16(a[u].x, a[u].y), pack_bf16(a[u].z, a[u].w)});
         return;
     }
     const int64_t e1 = e0 + kPassChunk < n ? e0 + kPassChunk : n;
