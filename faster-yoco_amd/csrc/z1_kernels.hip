@@ -104,6 +104,7 @@ struct AdamK {
 // Streams go through the global address space (global_load/global_store, not flat): the pointers come out of a
 // table in memory, so the compiler cannot infer the address space by itself.  The big streams carry nontemporal
 // hints: they are far larger than L2 and the MALL and are touched once (measured: 2.43 vs 2.10 ms without them).
+// The update's big stores go out through st_stream below, which adds the system-scope bits.
 #define Z1_GLOBAL __attribute__((address_space(1)))
 
 template <typename T>
