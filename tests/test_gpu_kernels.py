@@ -114,6 +114,21 @@ def test_adam_nonzero_moments_and_tails(pkg, dev, step):
     check_rows(rows, got, False, None, step)
 
 
+@pytest.mark.parametrize('nrows', [63, 64, 65, 200])
+@pytest.mark.parametrize('g_bf16', [False, True])
+def test_adam_tables_either_side_of_the_row_search(pkg, dev, nrows, g_bf16):
+    """A wave finds its chunk's row by binary search in tables of up to 64 rows and from the chunk -> row map in
+    larger ones: rows of random sizes (below one chunk, off the 256-element chunk, several chunks), bit-exact."""
+    rng = np.random.default_rng(900 + nrows)
+    sizes = rng.integers(1, 3000, nrows)
+    rows = []
+    for i, n in enumerate(sizes):
+        g, p, m, v = rand_state(int(n), 1000 + i)
+        rows.append((oracle.bf16_rne(g) if g_bf16 else g, p, m, v))
+    got = run_adam_rows(pkg, dev, rows, g_bf16, factor=0.8125, step=12)
+    check_rows(rows, got, g_bf16, 0.8125, 12)
+
+
 def test_adam_misaligned_rows_use_the_element_path(pkg, dev):
     sizes = [4096 * 3, 5000, 17]
     rows = [rand_state(n, 300 + i) for i, n in enumerate(sizes)]
