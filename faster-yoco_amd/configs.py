@@ -185,8 +185,8 @@ _BASELINE_FIELDS = {'p': 0, 'm': 1, 'v': 2, 'g': 3, 'outliers': 4}      # contri
 
 def baseline_inputs(name, seed=0, pieces=64, threads=None):
     """Full-size NumPy inputs of config `name` with BASELINE.json's distributions -- p ~ N(0, 0.02), the config's
-    m ~ N(0, m_std), v = |N(0, v_std)|, g ~ N(0, g_std) (c5: Student-t(2) x 1e-3 from the closed form of SURVEY
-    §8(d), exactly round(1e-3 n) entries set to +-1e4; c3: eight BF16 contributions ~ N(0, 1e-4), no g) -- as float32
+    m ~ N(0, m_std), v = |N(0, v_std)|, g ~ N(0, g_std) (c5: Student-t(2) x 1e-3, drawn as the closed-form inverse of
+    its CDF, exactly round(1e-3 n) entries set to +-1e4; c3: eight BF16 contributions ~ N(0, 1e-4), no g) -- as float32
     (contributions as uint16 bf16 bits).  Each field is cut into `pieces` fixed pieces, each drawn from its own PCG64
     stream seeded by (seed, field, piece), so the bits do not depend on `threads` (NumPy releases the GIL while it
     fills and computes, so the pieces run in parallel)."""
