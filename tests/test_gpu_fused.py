@@ -265,6 +265,51 @@ def test_adam_writes_the_scaled_gradients(pkg, dev, mode):
                       mode, g32=[outs[0][1:]] + outs[1:])
 
 
+@pytest.mark.parametrize('nrows', [20, 90])
+def test_gradient_outputs_either_side_of_the_row_search(pkg, dev, nrows):
+    """BF16 gradients x factor in, FP32 gradients written, over tables whose rows are found by binary search (up to
+    64 rows) and from the chunk -> row map (more): each row's output is the one of its own row (rows without an
+    output, empty rows and sizes off the chunk among them), bit-exact, and nothing is written outside them."""
+    from faster_yoco_amd import ops
+    rng = np.random.default_rng(40 + nrows)
+    sizes = [0 if i % 13 == 5 else int(n) for i, n in enumerate(rng.integers(1, 2500, nrows))]
+    gen = torch.Generator(device='cpu').manual_seed(nrows)
+    g16 = [(torch.randn(n, generator=gen) * 1e-2).to(torch.bfloat16).to(dev) for n in sizes]
+    p = [(torch.randn(n, generator=gen) * 0.02).to(dev) for n in sizes]
+    m = [(torch.randn(n, generator=gen) * 1e-4).to(dev) for n in sizes]
+    v = [(torch.randn(n, generator=gen) * 1e-8).abs().to(dev) for n in sizes]
+    p16 = [torch.zeros(n, dtype=torch.bfloat16, device=dev) for n in sizes]
+    raw = torch.full((sum(sizes) + 2,), -7.0, device=dev)
+    outs, off = [], 1
+    for i, n in enumerate(sizes):
+        outs.append(torch.empty(0, device=dev) if i % 7 == 3 else raw[off:off + n])
+        off += n
+    keep = [(g.view(torch.int16).cpu().numpy().view(np.uint16).copy(), a.cpu().numpy().copy(),
+             b.cpu().numpy().copy(), c.cpu().numpy().copy()) for g, a, b, c in zip(g16, p, m, v)]
+    factor = torch.tensor([0.71], device=dev)
+    fac = float(factor.item())
+    table = ops.Table([r + (r[0].numel(),) for r in zip(g16, p, m, v, p16)], dev)
+    hp = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    bc1, bc2 = ops.bias_corrections(hp['beta1'], hp['beta2'], 4)
+    ops.adam_cast(table, factor, hp['lr'], hp['beta1'], hp['beta2'], hp['eps'], bc1, bc2, hp['weight_decay'], 1,
+                  g32=outs)
+    torch.cuda.synchronize()
+    for i, (gb, p0, m0, v0) in enumerate(keep):
+        po, mo, vo, p16o = oracle.adam_cast(gb, p0, m0, v0, step=4, mode=1, factor=fac, **hp)
+        assert np.array_equal(f32_bits(p[i]), po.view(np.uint32)), i
+        assert np.array_equal(f32_bits(m[i]), mo.view(np.uint32)), i
+        assert np.array_equal(f32_bits(v[i]), vo.view(np.uint32)), i
+        assert np.array_equal(p16[i].view(torch.int16).cpu().numpy().view(np.uint16), p16o), i
+        if i % 7 != 3:
+            assert np.array_equal(f32_bits(outs[i]), oracle.scale_up(gb, fac).view(np.uint32)), i
+    assert raw[0].item() == -7.0 and raw[-1].item() == -7.0
+    for i, n in enumerate(sizes):                        # the rows without an output left their span of raw alone
+        if i % 7 == 3 and n:
+            o = 1 + sum(sizes[:i])
+            assert bool((raw[o:o + n] == -7.0).all()), i
+    table.close()
+
+
 @pytest.mark.parametrize('total', [300_000, 150_000_000])
 def test_bf16_norm_pass(pkg, dev, total):
     """The norm pass over BF16 gradients (chunk pairs, one 128-bit load per lane where a pair is whole and aligned,
